@@ -1,0 +1,279 @@
+#!/usr/bin/env python3
+"""Benchmark of grout's attention hot path on one MI355X.
+
+Primary line (BASELINE.json metric): decode-attention HBM GB/s on the
+Qwen3-32B-shaped decode step at 32k context (Hq=64, Hkv=8, D=128), one step =
+split-K decode + LSE merge for one layer; the step rotates over 4 layer caches
+(4 x 128 MiB of K+V > the 256 MB Infinity Cache) so K/V stream from HBM.
+Also reported: prefill FMHA TFLOP/s (Qwen3-4B, S=2048), the 4B decode layer
+and 36-layer graph step (ctx 4096), the fused QK-norm/RoPE/KV write, and the
+CPU oracle baseline timed on this host.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+F16_MFMA_PEAK_TFLOPS = 2516.6  # MI355X dense fp16 MFMA, TFLOP/s
+D = 128
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--only", default="", help="comma list: decode32b,prefill,decode4b,norm")
+    return ap.parse_args()
+
+
+def time_launches(fn, steps, warmup, stream=None, graph=True):
+    """Average device time per call of fn(i) over `steps` back-to-back calls,
+    bracketed by HIP events recorded on the stream the kernels are launched on.
+    With graph=True the `steps` calls are first captured into one HIP graph
+    (the C ABI calls are capture-safe) so host launch overhead cannot leave the
+    GPU idle between calls; the timed region is one replay of that graph."""
+    import torch
+
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    if graph:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(steps):
+                fn(i)
+        g.replay()  # untimed replay
+        torch.cuda.synchronize()
+        s = torch.cuda.current_stream()
+        start.record(s)
+        g.replay()
+        end.record(s)
+    else:
+        s = stream or torch.cuda.current_stream()
+        start.record(s)
+        for i in range(steps):
+            fn(i)
+        end.record(s)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    if graph:
+        del g
+    return ms
+
+
+def bench_decode(ops, Hq, Hkv, ctx, max_ctx, n_layers, steps, warmup, num_splits=None):
+    import torch
+
+    dev = torch.device("cuda")
+    stream = torch.cuda.current_stream(dev)
+    g = torch.Generator(device=dev).manual_seed(1234)
+    kcs = [torch.randn((Hkv, max_ctx, D), generator=g, device=dev, dtype=torch.float16)
+           for _ in range(n_layers)]
+    vcs = [torch.randn((Hkv, max_ctx, D), generator=g, device=dev, dtype=torch.float16)
+           for _ in range(n_layers)]
+    q = torch.randn((Hq, D), generator=g, device=dev, dtype=torch.float16)
+    out = torch.empty_like(q)
+    pos = torch.tensor([ctx - 1], dtype=torch.int32, device=dev)
+    ns = num_splits or ops.default_splits(max_ctx, Hq, Hkv)
+    ws = ops.decode_workspace(Hq, Hkv, ns, dev)
+    G = Hq // Hkv
+    acc = ws[: Hkv * ns * G * D].view(Hkv, ns, G, D)
+    ml = ws[Hkv * ns * G * D:].view(Hkv, ns, G, 2)
+
+    def step(i=0):
+        j = i % n_layers
+        ops.attn_decode(q, kcs[j], vcs[j], pos, num_splits=ns, out=out, workspace=ws)
+
+    from grout_amd._lib import call
+    import ctypes as C
+
+    qp, pp = C.c_void_p(q.data_ptr()), C.c_void_p(pos.data_ptr())
+    kps = [C.c_void_p(t.data_ptr()) for t in kcs]
+    vps = [C.c_void_p(t.data_ptr()) for t in vcs]
+    ap, mp = C.c_void_p(acc.data_ptr()), C.c_void_p(ml.data_ptr())
+
+    def split_only(i=0):
+        j = i % n_layers
+        sp = C.c_void_p(torch.cuda.current_stream().cuda_stream)  # the capture stream
+        call("grout_fmha_decode_gqa_split", qp, kps[j], vps[j], ap, mp, pp, Hq, Hkv, D, max_ctx,
+             max_ctx * D, ns, 1.0 / math.sqrt(D), sp)
+
+    step_ms = time_launches(step, steps, warmup, stream)
+    split_ms = time_launches(split_only, steps, warmup, stream)
+    alg_bytes = 2 * Hkv * ctx * D * 2 + 2 * Hq * D * 2
+    del kcs, vcs
+    torch.cuda.empty_cache()
+    return dict(step_ms=step_ms, split_ms=split_ms, alg_bytes=alg_bytes, num_splits=ns)
+
+
+def bench_decode_graph(grout_amd, Hq, Hkv, ctx, max_ctx, n_layers, steps, warmup):
+    import torch
+    from grout_amd.engine import AttentionConfig, AttentionEngine
+
+    dev = torch.device("cuda")
+    cfg = AttentionConfig(n_layers, Hq, Hkv, max_ctx=max_ctx)
+    ones = [torch.ones(D, dtype=torch.float16, device=dev) for _ in range(n_layers)]
+    eng = AttentionEngine(cfg, ones, ones, dev)
+    g = torch.Generator(device=dev).manual_seed(7)
+    for t in eng.k_caches + eng.v_caches:
+        t.normal_(generator=g)
+    graph = eng.build_decode_graph()
+    for b in graph.qkv:
+        b.normal_(generator=g)
+    stream = torch.cuda.current_stream(dev)
+    ms = time_launches(lambda i=0: graph.launch_step(ctx - 1), steps, warmup, stream, graph=False)
+    graph.destroy()
+    del eng
+    torch.cuda.empty_cache()
+    return ms
+
+
+def bench_prefill(ops, S, Hq, Hkv, steps, warmup):
+    import torch
+
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(99)
+    q = torch.randn((S, Hq, D), generator=g, device=dev, dtype=torch.float16)
+    kc = torch.randn((Hkv, S, D), generator=g, device=dev, dtype=torch.float16)
+    vc = torch.randn((Hkv, S, D), generator=g, device=dev, dtype=torch.float16)
+    out = torch.empty_like(q)
+    ms = time_launches(lambda i=0: ops.fmha_prefill(q, kc, vc, 0, out=out), steps, warmup,
+                       torch.cuda.current_stream(dev))
+    flop = 4.0 * Hq * D * S * (S + 1) / 2
+    return dict(ms=ms, flop=flop)
+
+
+def bench_norm(ops, S, Hq, Hkv, max_ctx, steps, warmup):
+    import torch
+
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(5)
+    q = torch.randn((S, Hq, D), generator=g, device=dev, dtype=torch.float16)
+    k = torch.randn((S, Hkv, D), generator=g, device=dev, dtype=torch.float16)
+    v = torch.randn((S, Hkv, D), generator=g, device=dev, dtype=torch.float16)
+    gam = torch.ones(D, dtype=torch.float16, device=dev)
+    rope = ops.rope_tables(max_ctx, device=dev)
+    kc = torch.zeros((Hkv, max_ctx, D), dtype=torch.float16, device=dev)
+    vc = torch.zeros_like(kc)
+    out = torch.empty_like(q)
+    ms = time_launches(lambda i=0: ops.qk_norm_rope_kv_prefill(q, k, v, gam, gam, rope, kc, vc, 0,
+                                                               out=out),
+                       steps, warmup, torch.cuda.current_stream(dev))
+    alg_bytes = 2 * S * (Hq + 2 * Hkv) * D * 2
+    return dict(ms=ms, alg_bytes=alg_bytes)
+
+
+def cpu_baseline_decode(Hq, Hkv, ctx):
+    """Scalar fp32 oracle (single thread) on one 32B decode layer: 16 of the 64
+    query heads (2 kv heads) at full context; GB/s scaled to the whole layer."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import oracle as O
+
+    hq_s, hkv_s = 16, 2
+    q = O.fill_normal_f16(O.seed_for("bq"), (hq_s, D))
+    kc = O.fill_normal_f16(O.seed_for("bk"), (hkv_s, ctx, D))
+    vc = O.fill_normal_f16(O.seed_for("bv"), (hkv_s, ctx, D))
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        O.attention_decode(q, kc, vc, ctx - 1, nthreads=1)
+        reps += 1
+        if time.perf_counter() - t0 > 10.0:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    layer_s = dt * (Hq / hq_s)
+    alg_bytes = 2 * Hkv * ctx * D * 2 + 2 * Hq * D * 2
+    return dict(value=alg_bytes / layer_s / 1e9, unit="GB/s", cores=1, kind="port",
+                sample=f"oracle/grout_oracle.c go_attention_decode, 1 thread, {hq_s} q heads x "
+                       f"{hkv_s} kv heads at ctx {ctx} ({reps} reps, {dt*1e3:.1f} ms each), "
+                       f"scaled x{Hq // hq_s} to the full Hq={Hq} layer",
+                layer_ms=layer_s * 1e3)
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path "
+              f"(requested --gpus {a.gpus}); run with --gpus 1", file=sys.stderr)
+        return 2
+    import torch
+    import grout_amd
+    from grout_amd import ops
+
+    grout_amd.lib()
+    only = set(filter(None, a.only.split(",")))
+    want = lambda k: not only or k in only
+    res = {}
+    if want("decode32b"):
+        res["decode32b"] = bench_decode(ops, 64, 8, 32768, 32768, 4, a.steps, a.warmup)
+        print(f"# decode32b {res['decode32b']}", file=sys.stderr, flush=True)
+    if want("prefill"):
+        res["prefill"] = bench_prefill(ops, 2048, 32, 8, max(a.steps // 4, 10), a.warmup)
+        print(f"# prefill {res['prefill']}", file=sys.stderr, flush=True)
+    if want("decode4b"):
+        res["decode4b"] = bench_decode(ops, 32, 8, 4096, 32768, 36, a.steps, a.warmup)
+        res["graph4b_ms"] = bench_decode_graph(grout_amd, 32, 8, 4096, 32768, 36,
+                                               max(a.steps // 4, 10), a.warmup)
+        print(f"# decode4b {res['decode4b']} graph {res['graph4b_ms']}", file=sys.stderr, flush=True)
+    if want("norm"):
+        res["norm"] = bench_norm(ops, 2048, 32, 8, 32768, a.steps, a.warmup)
+        print(f"# norm {res['norm']}", file=sys.stderr, flush=True)
+
+    line = {"metric": "decode-attn HBM GB/s (% of peak) + prefill FMHA TFLOP/s (% MFMA peak)",
+            "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic"}
+    if "decode32b" in res:
+        r = res["decode32b"]
+        gbs = r["alg_bytes"] / (r["step_ms"] * 1e-3) / 1e9
+        split_gbs = r["alg_bytes"] / (r["split_ms"] * 1e-3) / 1e9
+        line.update(value=round(gbs, 1), unit="GB/s", ms_per_step=round(r["step_ms"], 5))
+        line["config"] = {"workload": "qwen3-32b decode attention (split-K + LSE merge), Hq=64 "
+                                      "Hkv=8 D=128, ctx 32768, batch 1, 4 rotating layer caches",
+                          "num_splits": r["num_splits"], "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        line["roofline"] = {"bound": "hbm", "kernel": "attn_decode_split_kernel",
+                            "achieved": round(split_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": round(split_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                            "kernel_us": round(r["split_ms"] * 1e3, 3),
+                            "alg_bytes_per_launch": r["alg_bytes"]}
+    if "prefill" in res:
+        r = res["prefill"]
+        tf = r["flop"] / (r["ms"] * 1e-3) / 1e12
+        line["prefill"] = {"workload": "qwen3-4b causal prefill FMHA S=2048 Hq=32 Hkv=8 D=128",
+                           "us": round(r["ms"] * 1e3, 2), "tflops": round(tf, 1),
+                           "mfma_frac": round(tf / F16_MFMA_PEAK_TFLOPS, 4),
+                           "flop": r["flop"]}
+    if "decode4b" in res:
+        r = res["decode4b"]
+        gbs = r["alg_bytes"] / (r["step_ms"] * 1e-3) / 1e9
+        line["decode4b"] = {"workload": "qwen3-4b decode attention Hq=32 Hkv=8 ctx 4096, 36 layer caches",
+                            "us_per_layer": round(r["step_ms"] * 1e3, 2), "gbs": round(gbs, 1),
+                            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "num_splits": r["num_splits"],
+                            "graph_36_layers_us": round(res["graph4b_ms"] * 1e3, 1)}
+    if "norm" in res:
+        r = res["norm"]
+        gbs = r["alg_bytes"] / (r["ms"] * 1e-3) / 1e9
+        line["qk_norm_rope_kv"] = {"workload": "fused QK-norm/RoPE/KV write S=2048 Hq=32 Hkv=8",
+                                   "us": round(r["ms"] * 1e3, 2), "gbs": round(gbs, 1),
+                                   "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    if not a.no_cpu and "decode32b" in res:
+        cb = cpu_baseline_decode(64, 8, 32768)
+        line["cpu_baseline"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in cb.items()}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

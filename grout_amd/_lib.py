@@ -1,0 +1,86 @@
+"""ctypes binding of grout_amd/libgrout_attn.so (the C ABI in include/grout_attn.h).
+
+The library is the only compute path: if it is missing this module raises, it
+never falls back to PyTorch or CPU code.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libgrout_attn.so")
+_lock = threading.Lock()
+_lib = None
+
+
+class GroutError(RuntimeError):
+    """A C ABI call returned a non-zero status (message from grout_last_error)."""
+
+    def __init__(self, fn: str, code: int, msg: str):
+        super().__init__(f"{fn} failed ({code}): {msg}")
+        self.code = code
+
+
+_p, _i, _l, _f, _sz, _u32 = C.c_void_p, C.c_int, C.c_long, C.c_float, C.c_size_t, C.c_uint32
+
+
+class DecodeLayer(C.Structure):
+    _fields_ = [("qkv", _p), ("gamma_q", _p), ("gamma_k", _p), ("q_rope", _p),
+                ("k_cache", _p), ("v_cache", _p), ("attn_out", _p)]
+
+
+# name -> (restype, argtypes).  Every symbol declared in include/grout_attn.h.
+SIGNATURES = {
+    "grout_last_error": (C.c_char_p, []),
+    "grout_abi_version": (_i, []),
+    "grout_rope_inv_freq": (_i, [_i, _f, _p]),
+    "grout_rope_table_host": (_i, [_i, _i, _f, _p, _p]),
+    "grout_qk_norm_rope_kv_prefill": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i,
+                                           _i, _i, _l, _f, _p]),
+    "grout_qk_norm_rope_kv_decode": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _l,
+                                          _f, _p]),
+    "grout_fmha_prefill": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i, _l, _f, _p]),
+    "grout_attn_decode_default_splits": (_i, [_i, _i, _i]),
+    "grout_attn_decode_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "grout_attn_decode": (_i, [_p, _p, _p, _p, _p, _sz, _p, _i, _i, _i, _i, _l, _i, _f, _p]),
+    "grout_fmha_decode_gqa_split": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _l, _i, _f, _p]),
+    "grout_splitk_reduce_merge": (_i, [_p, _p, _p, _i, _i, _i, _i, _p]),
+    "grout_decode_graph_create": (_i, [C.POINTER(DecodeLayer), _i, _p, _p, _p, _sz, _i, _i, _i,
+                                       _i, _i, _f, _f, _p, C.POINTER(_p)]),
+    "grout_decode_graph_launch": (_i, [_p, _u32, _p]),
+    "grout_decode_graph_position_ptr": (_p, [_p]),
+    "grout_decode_graph_destroy": (_i, [_p]),
+    "grout_diag_mfma_layout": (_i, [_p, _p]),
+}
+
+
+def lib():
+    """Load the HIP library (raises if it has not been built)."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"{LIB_PATH} is missing: build the gfx950 HIP library with "
+                    "`python -m grout_amd.build` (there is no fallback path)")
+            L = C.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(L, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return lib().grout_last_error().decode()
+
+
+def call(name: str, *args) -> int:
+    """Call a status-returning ABI function; raise GroutError on failure."""
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        raise GroutError(name, rc, last_error())
+    return rc

@@ -1,0 +1,378 @@
+// C ABI of the gfx950 attention hot path: argument validation (the
+// reference's `ensure!` checks before each launch), split selection, RoPE
+// tables and the decode-step HIP graph runner.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+
+#include "../../include/grout_attn.h"
+#include "kernels.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return GROUT_OK;
+  fail((int)e, "%s: %s", what, hipGetErrorString(e));
+  return (int)e;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_heads(int hq, int hkv, int head_dim, int max_group) {
+  if (head_dim != 128)
+    return fail(GROUT_ENOTSUP, "head_dim=%d: only 128 is supported (src/model.rs:1446)", head_dim);
+  if (hq <= 0 || hkv <= 0 || hq % hkv != 0)
+    return fail(GROUT_EINVAL, "num_q_heads=%d must be a positive multiple of num_kv_heads=%d", hq,
+                hkv);
+  if (hq / hkv > max_group)
+    return fail(GROUT_ENOTSUP, "GQA group %d exceeds %d", hq / hkv, max_group);
+  return GROUT_OK;
+}
+
+#define GROUT_CHECK(expr)           \
+  do {                              \
+    const int _rc = (expr);         \
+    if (_rc != GROUT_OK) return _rc; \
+  } while (0)
+
+#define GROUT_NEED(cond, code, ...)                   \
+  do {                                                \
+    if (!(cond)) return fail((code), __VA_ARGS__);    \
+  } while (0)
+
+int check_ptrs16(std::initializer_list<std::pair<const void*, const char*>> ptrs) {
+  for (const auto& p : ptrs) {
+    if (p.first == nullptr) return fail(GROUT_EINVAL, "%s is NULL", p.second);
+    if (!aligned16(p.first)) return fail(GROUT_EALIGN, "%s is not 16-byte aligned", p.second);
+  }
+  return GROUT_OK;
+}
+
+int check_stride(long kv_head_stride, long min_rows) {
+  GROUT_NEED(kv_head_stride % 8 == 0, GROUT_EALIGN,
+             "kv_head_stride=%ld elements is not a multiple of 8 (16 bytes)", kv_head_stride);
+  GROUT_NEED(kv_head_stride >= min_rows * 128, GROUT_EINVAL,
+             "kv_head_stride=%ld is smaller than %ld rows of 128", kv_head_stride, min_rows);
+  return GROUT_OK;
+}
+
+constexpr int kMaxDecodeGroup = 16;
+constexpr int kMaxSplits = 4096;
+
+size_t decode_ws_bytes(int hq, int hkv, int nsplit) {
+  const size_t g = (size_t)(hq / hkv);
+  return (size_t)hkv * nsplit * g * (128 + 2) * sizeof(float);
+}
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace
+
+extern "C" {
+
+const char* grout_last_error(void) { return g_last_error.c_str(); }
+
+int grout_abi_version(void) { return (1 << 16) | 0; }
+
+int grout_rope_inv_freq(int head_dim, float theta, float* inv_freq) {
+  GROUT_NEED(head_dim > 0 && head_dim % 2 == 0, GROUT_EINVAL, "head_dim=%d must be even",
+             head_dim);
+  GROUT_NEED(std::isfinite(theta) && theta > 0.f, GROUT_EINVAL, "rope theta=%g", (double)theta);
+  GROUT_NEED(inv_freq != nullptr, GROUT_EINVAL, "inv_freq is NULL");
+  for (int i = 0; i < head_dim; i += 2) {
+    const float p = (float)i / (float)head_dim;
+    inv_freq[i / 2] = 1.0f / powf(theta, p);
+  }
+  return GROUT_OK;
+}
+
+int grout_rope_table_host(int max_ctx, int head_dim, float theta, float* cos_out,
+                          float* sin_out) {
+  GROUT_NEED(max_ctx > 0, GROUT_EINVAL, "max_ctx=%d", max_ctx);
+  GROUT_NEED(cos_out != nullptr && sin_out != nullptr, GROUT_EINVAL, "table pointer is NULL");
+  const int half = head_dim / 2;
+  float inv[512];
+  GROUT_NEED(half <= 512, GROUT_ENOTSUP, "head_dim=%d too large", head_dim);
+  GROUT_CHECK(grout_rope_inv_freq(head_dim, theta, inv));
+  for (int p = 0; p < max_ctx; ++p) {
+    const float pf = (float)p;
+    for (int i = 0; i < half; ++i) {
+      const float ang = pf * inv[i];
+      cos_out[(size_t)p * half + i] = (float)std::cos((double)ang);
+      sin_out[(size_t)p * half + i] = (float)std::sin((double)ang);
+    }
+  }
+  return GROUT_OK;
+}
+
+int grout_qk_norm_rope_kv_prefill(const void* q, const void* k, const void* v,
+                                  const void* gamma_q, const void* gamma_k,
+                                  const float* rope_cos, const float* rope_sin, void* q_out,
+                                  void* k_cache, void* v_cache, int pos0, int seq_len,
+                                  int num_q_heads, int num_kv_heads, int head_dim, int max_ctx,
+                                  long kv_head_stride, float eps, void* stream) {
+  GROUT_CHECK(check_heads(num_q_heads, num_kv_heads, head_dim, 1 << 20));
+  GROUT_NEED(seq_len >= 1, GROUT_EINVAL, "prefill requires at least one token");
+  GROUT_NEED(pos0 >= 0 && (long)pos0 + seq_len <= max_ctx, GROUT_EINVAL,
+             "fused qk/rope/kv range [%d..%ld) exceeds max_seq_len %d", pos0,
+             (long)pos0 + seq_len, max_ctx);
+  GROUT_NEED(std::isfinite(eps) && eps > 0.f, GROUT_EINVAL, "rms_norm_eps=%g must be positive",
+             (double)eps);
+  GROUT_CHECK(check_ptrs16({{q, "q"}, {k, "k"}, {v, "v"}, {gamma_q, "gamma_q"},
+                            {gamma_k, "gamma_k"}, {rope_cos, "rope_cos"},
+                            {rope_sin, "rope_sin"}, {q_out, "q_out"}, {k_cache, "k_cache"},
+                            {v_cache, "v_cache"}}));
+  GROUT_CHECK(check_stride(kv_head_stride, max_ctx));
+  return hip_status(grout::launch_qk_norm_rope_kv_prefill(
+                        q, k, v, gamma_q, gamma_k, rope_cos, rope_sin, q_out, k_cache, v_cache,
+                        pos0, seq_len, num_q_heads, num_kv_heads, kv_head_stride, max_ctx, eps,
+                        as_stream(stream)),
+                    "qk_norm_rope_kv_prefill launch");
+}
+
+int grout_qk_norm_rope_kv_decode(const void* qkv, const void* gamma_q, const void* gamma_k,
+                                 const float* rope_cos, const float* rope_sin, void* q_out,
+                                 void* k_cache, void* v_cache, const uint32_t* d_pos,
+                                 int num_q_heads, int num_kv_heads, int head_dim, int max_ctx,
+                                 long kv_head_stride, float eps, void* stream) {
+  GROUT_CHECK(check_heads(num_q_heads, num_kv_heads, head_dim, 1 << 20));
+  GROUT_NEED(max_ctx >= 1, GROUT_EINVAL, "max_ctx=%d", max_ctx);
+  GROUT_NEED(std::isfinite(eps) && eps > 0.f, GROUT_EINVAL, "rms_norm_eps=%g must be positive",
+             (double)eps);
+  GROUT_NEED(d_pos != nullptr, GROUT_EINVAL, "d_pos is NULL");
+  GROUT_CHECK(check_ptrs16({{qkv, "qkv"}, {gamma_q, "gamma_q"}, {gamma_k, "gamma_k"},
+                            {rope_cos, "rope_cos"}, {rope_sin, "rope_sin"}, {q_out, "q_out"},
+                            {k_cache, "k_cache"}, {v_cache, "v_cache"}}));
+  GROUT_CHECK(check_stride(kv_head_stride, max_ctx));
+  return hip_status(grout::launch_qk_norm_rope_kv_decode(
+                        qkv, gamma_q, gamma_k, rope_cos, rope_sin, q_out, k_cache, v_cache,
+                        d_pos, num_q_heads, num_kv_heads, kv_head_stride, max_ctx, eps,
+                        as_stream(stream)),
+                    "qk_norm_rope_kv_decode launch");
+}
+
+int grout_fmha_prefill(const void* q, const void* k_cache, const void* v_cache, void* out,
+                       int seq_len, int pos0, int num_q_heads, int num_kv_heads, int head_dim,
+                       long kv_head_stride, float qk_scale, void* stream) {
+  GROUT_CHECK(check_heads(num_q_heads, num_kv_heads, head_dim, 1 << 20));
+  GROUT_NEED(seq_len >= 1, GROUT_EINVAL, "attention requires q_len >= 1");
+  GROUT_NEED(pos0 >= 0, GROUT_EINVAL, "pos0=%d", pos0);
+  GROUT_NEED(std::isfinite(qk_scale) && qk_scale > 0.f, GROUT_EINVAL, "qk_scale=%g",
+             (double)qk_scale);
+  GROUT_CHECK(check_ptrs16({{q, "q"}, {k_cache, "k_cache"}, {v_cache, "v_cache"}, {out, "out"}}));
+  GROUT_CHECK(check_stride(kv_head_stride, (long)pos0 + seq_len));
+  return hip_status(grout::launch_fmha_prefill(q, k_cache, v_cache, out, seq_len, pos0,
+                                               num_q_heads, num_kv_heads, kv_head_stride,
+                                               qk_scale, as_stream(stream)),
+                    "fmha_prefill launch");
+}
+
+int grout_attn_decode_default_splits(int ctx_len, int num_q_heads, int num_kv_heads) {
+  if (ctx_len < 1 || num_kv_heads < 1) return 1;
+  (void)num_q_heads;
+  const int tiles = (ctx_len + 31) / 32;
+  // About 512 workgroups (two per CU) at long context; at least 8 tiles
+  // (2 per wave) per workgroup so short contexts do not scatter into empty splits.
+  int by_work = (tiles + 7) / 8;
+  int by_grid = (512 + num_kv_heads - 1) / num_kv_heads;
+  int n = by_work < by_grid ? by_work : by_grid;
+  if (n < 1) n = 1;
+  if (n > kMaxSplits) n = kMaxSplits;
+  return n;
+}
+
+size_t grout_attn_decode_workspace_bytes(int num_q_heads, int num_kv_heads, int head_dim,
+                                         int num_splits) {
+  if (head_dim != 128 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
+      num_splits <= 0)
+    return 0;
+  return decode_ws_bytes(num_q_heads, num_kv_heads, num_splits);
+}
+
+int grout_fmha_decode_gqa_split(const void* q, const void* k_cache, const void* v_cache,
+                                float* part_acc, float* part_ml, const uint32_t* d_pos,
+                                int num_q_heads, int num_kv_heads, int head_dim, int max_ctx,
+                                long kv_head_stride, int num_splits, float qk_scale,
+                                void* stream) {
+  GROUT_CHECK(check_heads(num_q_heads, num_kv_heads, head_dim, kMaxDecodeGroup));
+  GROUT_NEED(max_ctx >= 1, GROUT_EINVAL, "max_ctx=%d", max_ctx);
+  GROUT_NEED(num_splits >= 1 && num_splits <= kMaxSplits, GROUT_EINVAL,
+             "num_splits=%d outside [1, %d]", num_splits, kMaxSplits);
+  GROUT_NEED(std::isfinite(qk_scale) && qk_scale > 0.f, GROUT_EINVAL, "qk_scale=%g",
+             (double)qk_scale);
+  GROUT_NEED(d_pos != nullptr, GROUT_EINVAL, "d_pos is NULL");
+  GROUT_CHECK(check_ptrs16({{q, "q"}, {k_cache, "k_cache"}, {v_cache, "v_cache"},
+                            {part_acc, "part_acc"}, {part_ml, "part_ml"}}));
+  GROUT_CHECK(check_stride(kv_head_stride, max_ctx));
+  return hip_status(grout::launch_attn_decode_split(q, k_cache, v_cache, kv_head_stride, d_pos,
+                                                    max_ctx, num_q_heads, num_kv_heads,
+                                                    num_splits, qk_scale, part_acc, part_ml,
+                                                    as_stream(stream)),
+                    "fmha_decode_gqa_split launch");
+}
+
+int grout_splitk_reduce_merge(const float* part_acc, const float* part_ml, void* out,
+                              int num_q_heads, int num_kv_heads, int head_dim, int num_splits,
+                              void* stream) {
+  GROUT_CHECK(check_heads(num_q_heads, num_kv_heads, head_dim, kMaxDecodeGroup));
+  GROUT_NEED(num_splits >= 1 && num_splits <= kMaxSplits, GROUT_EINVAL,
+             "num_splits=%d outside [1, %d]", num_splits, kMaxSplits);
+  GROUT_CHECK(check_ptrs16({{part_acc, "part_acc"}, {part_ml, "part_ml"}, {out, "out"}}));
+  return hip_status(grout::launch_attn_decode_merge(part_acc, part_ml, out, num_q_heads,
+                                                    num_kv_heads, num_splits,
+                                                    as_stream(stream)),
+                    "splitk_reduce_merge launch");
+}
+
+int grout_attn_decode(const void* q, const void* k_cache, const void* v_cache, void* out,
+                      void* workspace, size_t workspace_bytes, const uint32_t* d_pos,
+                      int num_q_heads, int num_kv_heads, int head_dim, int max_ctx,
+                      long kv_head_stride, int num_splits, float qk_scale, void* stream) {
+  GROUT_CHECK(check_heads(num_q_heads, num_kv_heads, head_dim, kMaxDecodeGroup));
+  if (num_splits <= 0) num_splits = grout_attn_decode_default_splits(max_ctx, num_q_heads, num_kv_heads);
+  GROUT_NEED(num_splits <= kMaxSplits, GROUT_EINVAL, "num_splits=%d > %d", num_splits, kMaxSplits);
+  const size_t need = decode_ws_bytes(num_q_heads, num_kv_heads, num_splits);
+  GROUT_NEED(workspace != nullptr && workspace_bytes >= need, GROUT_EINVAL,
+             "workspace of %zu bytes < %zu needed for %d splits", workspace_bytes, need,
+             num_splits);
+  GROUT_NEED(out != nullptr && aligned16(out), GROUT_EALIGN, "out is NULL or misaligned");
+  float* part_acc = static_cast<float*>(workspace);
+  const size_t G = (size_t)(num_q_heads / num_kv_heads);
+  float* part_ml = part_acc + (size_t)num_kv_heads * num_splits * G * 128;
+  GROUT_CHECK(grout_fmha_decode_gqa_split(q, k_cache, v_cache, part_acc, part_ml, d_pos,
+                                          num_q_heads, num_kv_heads, head_dim, max_ctx,
+                                          kv_head_stride, num_splits, qk_scale, stream));
+  return grout_splitk_reduce_merge(part_acc, part_ml, out, num_q_heads, num_kv_heads, head_dim,
+                                   num_splits, stream);
+}
+
+// ------------------------------------------------------------------ graph
+
+struct grout_decode_graph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  uint32_t* d_pos = nullptr;
+  int max_ctx = 0;
+};
+
+}  // extern "C"
+
+namespace {
+__global__ void set_position_kernel(uint32_t* d_pos, uint32_t value) { *d_pos = value; }
+}  // namespace
+
+extern "C" {
+
+int grout_decode_graph_create(const grout_decode_layer* layers, int num_layers,
+                              const float* rope_cos, const float* rope_sin, void* workspace,
+                              size_t workspace_bytes, int num_q_heads, int num_kv_heads,
+                              int head_dim, int max_ctx, int num_splits, float eps,
+                              float qk_scale, void* stream, grout_decode_graph** out) {
+  GROUT_NEED(out != nullptr, GROUT_EINVAL, "out is NULL");
+  *out = nullptr;
+  GROUT_NEED(layers != nullptr && num_layers >= 1, GROUT_EINVAL, "num_layers=%d", num_layers);
+  GROUT_CHECK(check_heads(num_q_heads, num_kv_heads, head_dim, kMaxDecodeGroup));
+  GROUT_NEED(max_ctx >= 1, GROUT_EINVAL, "max_ctx=%d", max_ctx);
+  if (num_splits <= 0) num_splits = grout_attn_decode_default_splits(max_ctx, num_q_heads, num_kv_heads);
+  const long stride = (long)max_ctx * 128;
+  // Validate every layer up front so a failed capture never leaves a half-built graph.
+  for (int i = 0; i < num_layers; ++i) {
+    const grout_decode_layer& L = layers[i];
+    const int rc = check_ptrs16({{L.qkv, "qkv"}, {L.gamma_q, "gamma_q"}, {L.gamma_k, "gamma_k"},
+                                 {L.q_rope, "q_rope"}, {L.k_cache, "k_cache"},
+                                 {L.v_cache, "v_cache"}, {L.attn_out, "attn_out"}});
+    if (rc != GROUT_OK) return fail(rc, "layer %d: %s", i, g_last_error.c_str());
+  }
+  const size_t need = decode_ws_bytes(num_q_heads, num_kv_heads, num_splits);
+  GROUT_NEED(workspace != nullptr && workspace_bytes >= need, GROUT_EINVAL,
+             "workspace of %zu bytes < %zu needed", workspace_bytes, need);
+
+  grout_decode_graph* g = new (std::nothrow) grout_decode_graph();
+  GROUT_NEED(g != nullptr, GROUT_EINVAL, "out of host memory");
+  g->max_ctx = max_ctx;
+  hipStream_t cap = nullptr;
+  int rc = hip_status(hipMalloc(&g->d_pos, sizeof(uint32_t)), "hipMalloc(position)");
+  if (rc == GROUT_OK) rc = hip_status(hipMemset(g->d_pos, 0, sizeof(uint32_t)), "hipMemset(position)");
+  if (rc == GROUT_OK)
+    rc = hip_status(hipStreamCreateWithFlags(&cap, hipStreamNonBlocking), "hipStreamCreate");
+  if (rc == GROUT_OK) {
+    rc = hip_status(hipStreamBeginCapture(cap, hipStreamCaptureModeThreadLocal), "BeginCapture");
+    if (rc == GROUT_OK) {
+      for (int i = 0; i < num_layers && rc == GROUT_OK; ++i) {
+        const grout_decode_layer& L = layers[i];
+        rc = grout_qk_norm_rope_kv_decode(L.qkv, L.gamma_q, L.gamma_k, rope_cos, rope_sin,
+                                          L.q_rope, L.k_cache, L.v_cache, g->d_pos, num_q_heads,
+                                          num_kv_heads, head_dim, max_ctx, stride, eps, cap);
+        if (rc == GROUT_OK)
+          rc = grout_attn_decode(L.q_rope, L.k_cache, L.v_cache, L.attn_out, workspace,
+                                 workspace_bytes, g->d_pos, num_q_heads, num_kv_heads, head_dim,
+                                 max_ctx, stride, num_splits, qk_scale, cap);
+      }
+      hipGraph_t graph = nullptr;
+      const hipError_t e = hipStreamEndCapture(cap, &graph);
+      if (rc == GROUT_OK) rc = hip_status(e, "EndCapture");
+      g->graph = graph;
+    }
+  }
+  if (rc == GROUT_OK)
+    rc = hip_status(hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0),
+                    "hipGraphInstantiate");
+  if (cap) (void)hipStreamDestroy(cap);
+  (void)stream;
+  if (rc != GROUT_OK) {
+    const std::string msg = g_last_error;
+    grout_decode_graph_destroy(g);
+    g_last_error = msg;
+    return rc;
+  }
+  *out = g;
+  return GROUT_OK;
+}
+
+int grout_decode_graph_launch(grout_decode_graph* graph, uint32_t position, void* stream) {
+  GROUT_NEED(graph != nullptr && graph->exec != nullptr, GROUT_EINVAL, "graph is NULL");
+  GROUT_NEED((long)position < (long)graph->max_ctx, GROUT_EINVAL,
+             "decode position %u exceeds max_ctx=%d", position, graph->max_ctx);
+  // The position travels as a kernel argument, so queued launches never race
+  // on a host staging buffer.
+  set_position_kernel<<<1, 1, 0, as_stream(stream)>>>(graph->d_pos, position);
+  GROUT_CHECK(hip_status(hipGetLastError(), "set position"));
+  return hip_status(hipGraphLaunch(graph->exec, as_stream(stream)), "hipGraphLaunch");
+}
+
+const uint32_t* grout_decode_graph_position_ptr(const grout_decode_graph* graph) {
+  return graph ? graph->d_pos : nullptr;
+}
+
+int grout_decode_graph_destroy(grout_decode_graph* graph) {
+  if (!graph) return GROUT_OK;
+  if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
+  if (graph->graph) (void)hipGraphDestroy(graph->graph);
+  if (graph->d_pos) (void)hipFree(graph->d_pos);
+  delete graph;
+  return GROUT_OK;
+}
+
+int grout_diag_mfma_layout(float* out, void* stream) {
+  GROUT_NEED(out != nullptr, GROUT_EINVAL, "out is NULL");
+  return hip_status(grout::launch_mfma_layout_probe(out, as_stream(stream)), "mfma probe");
+}
+
+}  // extern "C"

@@ -1,0 +1,45 @@
+// Device-side helpers shared by the gfx950 attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace grout {
+
+typedef _Float16 half_t;
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kHeadDim = 128;  // the reference enforces head_dim == 128 (src/model.rs:1446)
+constexpr int kWave = 64;
+
+// v_mfma_f32_16x16x32_f16.  Operand layout (lane l, 64 lanes):
+//   A (16 x 32): row l%16, k-slot l/16 holding 8 consecutive k values
+//   B (32 x 16): col l%16, same k-slot convention
+//   C (16 x 16): col l%16, rows 4*(l/16) + i, i = 0..3
+// Only the C layout matters for correctness as long as A and B fill their
+// k-slots with the same index order; that is how every kernel here uses it.
+__device__ __forceinline__ floatx4 mfma16x16x32(half8 a, half8 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ half8 as_half8(u32x4 v) { return __builtin_bit_cast(half8, v); }
+__device__ __forceinline__ u32x4 as_u32x4(half8 v) { return __builtin_bit_cast(u32x4, v); }
+
+// 16-byte global load that bypasses cache allocation for streamed data.
+__device__ __forceinline__ u32x4 load_stream16(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ u32x4 load16(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Cross-lane xor shuffle within the wave (ds_bpermute based).
+__device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+}  // namespace grout

@@ -1,0 +1,41 @@
+// Internal launch functions (C++ linkage) called by the C ABI layer in api.cpp.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace grout {
+
+hipError_t launch_qk_norm_rope_kv_prefill(const void* q, const void* k, const void* v,
+                                          const void* gamma_q, const void* gamma_k,
+                                          const float* rope_cos, const float* rope_sin,
+                                          void* q_out, void* k_cache, void* v_cache, int pos0,
+                                          int seq_len, int Hq, int Hkv, long head_stride,
+                                          int max_ctx, float eps, hipStream_t stream);
+
+hipError_t launch_qk_norm_rope_kv_decode(const void* qkv, const void* gamma_q,
+                                         const void* gamma_k, const float* rope_cos,
+                                         const float* rope_sin, void* q_out, void* k_cache,
+                                         void* v_cache, const uint32_t* d_pos, int Hq, int Hkv,
+                                         long head_stride, int max_ctx, float eps,
+                                         hipStream_t stream);
+
+// Split pass: part_acc [Hkv][nsplit][G][128] fp32 (unnormalized), part_ml
+// [Hkv][nsplit][G][2] fp32 (running max in log2 units, sum of exp2).
+hipError_t launch_attn_decode_split(const void* q, const void* k_cache, const void* v_cache,
+                                    long head_stride, const uint32_t* d_pos, int max_ctx,
+                                    int Hq, int Hkv, int nsplit, float qk_scale,
+                                    float* part_acc, float* part_ml, hipStream_t stream);
+
+hipError_t launch_attn_decode_merge(const float* part_acc, const float* part_ml, void* out,
+                                    int Hq, int Hkv, int nsplit, hipStream_t stream);
+
+hipError_t launch_fmha_prefill(const void* q, const void* k_cache, const void* v_cache,
+                               void* out, int seq_len, int pos0, int Hq, int Hkv,
+                               long head_stride, float qk_scale, hipStream_t stream);
+
+// Writes the 16x16 C fragment of A x B for A[i][k] = i*32+k (k < 32), B = I
+// padded, one float per (lane, element): used to confirm the MFMA lane layout.
+hipError_t launch_mfma_layout_probe(float* out64x4, hipStream_t stream);
+
+}  // namespace grout

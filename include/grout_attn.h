@@ -1,0 +1,197 @@
+/*
+ * grout_attn.h -- C ABI of the MI355X-native (gfx950) attention hot path of
+ * grout (rtburger/grout).  Plain C: pointers, sizes and status codes only.
+ *
+ * Conventions
+ *  - Every device pointer is caller-owned; head_dim must be 128 (the reference
+ *    enforces it at load, src/model.rs:1446).  fp16 tensors are passed as
+ *    `void*` to 16-byte-aligned device memory.
+ *  - KV caches use the reference layout [num_kv_heads][max_ctx][128] fp16
+ *    (src/model.rs:1587-1592).  `kv_head_stride` is the element distance
+ *    between kv heads (max_ctx*128 for such a cache).
+ *  - `stream` is a hipStream_t (NULL = default stream).  Every call is
+ *    asynchronous on that stream, allocates nothing, never synchronizes and
+ *    never reads device memory on the host, so it can be captured in a HIP
+ *    graph.  Calls are re-entrant; the only global state is a thread-local
+ *    error message.
+ *  - Return value: 0 on success, < 0 for an invalid argument (shape, stride,
+ *    alignment; the message is in grout_last_error()), > 0 a hipError_t.
+ *    This mirrors the reference's `ensure!` before every launch
+ *    (e.g. src/model.rs:4771-4854) and its anyhow::Result errors.
+ */
+#ifndef GROUT_ATTN_H
+#define GROUT_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GROUT_OK 0
+#define GROUT_EINVAL (-1)   /* bad shape / count / range                */
+#define GROUT_EALIGN (-2)   /* pointer or stride not 16-byte aligned    */
+#define GROUT_ENOTSUP (-3)  /* configuration this build does not handle */
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* grout_last_error(void);
+
+/* ABI version of this library: (major << 16) | minor. */
+int grout_abi_version(void);
+
+/* ------------------------------------------------------------------ */
+/* RoPE (a9)                                                          */
+/* ------------------------------------------------------------------ */
+
+/* Host function. inv_freq[i/2] = 1 / theta^(i/head_dim), i = 0,2,..., in f32.
+ * Replaces build_inv_freq (src/model.rs:7295-7306). */
+int grout_rope_inv_freq(int head_dim, float theta, float* inv_freq);
+
+/* Host function. cos/sin of the f32 angle (float)pos * inv_freq[i] for
+ * pos in [0, max_ctx), layout [max_ctx][head_dim/2] f32, each evaluated in
+ * double and rounded once.  The device kernels read these tables instead of
+ * evaluating cos/sin (the reference evaluates them per element,
+ * src/kernels.rs:5076-5082), which makes K-cache rows reproducible bit for
+ * bit on the CPU.  Upload the two arrays once per model. */
+int grout_rope_table_host(int max_ctx, int head_dim, float theta, float* cos_out,
+                          float* sin_out);
+
+/* ------------------------------------------------------------------ */
+/* Fused QK-RMSNorm + RoPE + KV-cache write (a1, a2)                   */
+/* ------------------------------------------------------------------ */
+
+/* Prefill: q [seq_len][Hq][128], k, v [seq_len][Hkv][128] (the projection
+ * outputs), gamma_q/gamma_k [128] fp16, rope tables [max_ctx][64] f32.
+ * Writes q_out [seq_len][Hq][128] and cache rows pos0 .. pos0+seq_len-1 of
+ * every kv head.  Requires pos0 + seq_len <= max_ctx.
+ * Replaces qk_norm_rope_kv_prefill_raw_f16 (src/kernels.rs:4837-5168) as
+ * launched by execute_qk_norm_rope_kv_prefill_op_ctx (src/model.rs:4753-4888),
+ * i.e. GraphOp::QkNormRopeKvPrefill (src/model.rs:773-779). */
+int grout_qk_norm_rope_kv_prefill(const void* q, const void* k, const void* v,
+                                  const void* gamma_q, const void* gamma_k,
+                                  const float* rope_cos, const float* rope_sin, void* q_out,
+                                  void* k_cache, void* v_cache, int pos0, int seq_len,
+                                  int num_q_heads, int num_kv_heads, int head_dim, int max_ctx,
+                                  long kv_head_stride, float eps, void* stream);
+
+/* Decode: qkv = [Q (Hq*128) | K (Hkv*128) | V (Hkv*128)] contiguous (the QKV
+ * GEMV output), position read from device memory d_pos[0] (u32).  Writes
+ * q_out [Hq][128] and cache row d_pos[0] of every kv head; a position
+ * >= max_ctx writes nothing.
+ * Replaces qk_norm_rope_kv_decode_raw_f16 (src/kernels.rs:5170-5452) as
+ * recorded in the decode graph (src/model.rs:3492-3519). */
+int grout_qk_norm_rope_kv_decode(const void* qkv, const void* gamma_q, const void* gamma_k,
+                                 const float* rope_cos, const float* rope_sin, void* q_out,
+                                 void* k_cache, void* v_cache, const uint32_t* d_pos,
+                                 int num_q_heads, int num_kv_heads, int head_dim, int max_ctx,
+                                 long kv_head_stride, float eps, void* stream);
+
+/* ------------------------------------------------------------------ */
+/* Causal GQA prefill attention (a3, a4, a7)                           */
+/* ------------------------------------------------------------------ */
+
+/* q [seq_len][Hq][128] post-RoPE, caches [Hkv][..][128] with
+ * kv_head_stride, out [seq_len][Hq][128].  Row s attends to kv positions
+ * 0 .. pos0+s (kv_len = pos0 + seq_len); kv head of q head h is h / (Hq/Hkv).
+ * qk_scale is normally 1/sqrt(128).
+ * Replaces fmha_prefill_causal / fmha_prefill_gqa / fmha_prefill_gqa_lpt
+ * (src/kernels.rs:2559-3298) as dispatched for GraphOp::Attention with a host
+ * position by attend_seq_arc_into_ctx_with_position (src/model.rs:6856-7134). */
+int grout_fmha_prefill(const void* q, const void* k_cache, const void* v_cache, void* out,
+                       int seq_len, int pos0, int num_q_heads, int num_kv_heads, int head_dim,
+                       long kv_head_stride, float qk_scale, void* stream);
+
+/* ------------------------------------------------------------------ */
+/* Split-K GQA decode attention + LSE merge (a5, a6)                   */
+/* ------------------------------------------------------------------ */
+
+/* Split count the library picks for a live context of ctx_len positions
+ * (the reference's FMHA_NUM_KV_SPLITS default / per-context overrides,
+ * src/model.rs:135-141). */
+int grout_attn_decode_default_splits(int ctx_len, int num_q_heads, int num_kv_heads);
+
+/* Bytes of fp32 scratch grout_attn_decode needs for num_splits splits:
+ * partial accumulators [Hkv][splits][G][128] + (max, sum) [Hkv][splits][G][2]. */
+size_t grout_attn_decode_workspace_bytes(int num_q_heads, int num_kv_heads, int head_dim,
+                                         int num_splits);
+
+/* q [Hq][128] post-RoPE (q head h = kvh*G + g, i.e. the [Hkv][G][128] grouped
+ * view), caches [Hkv][..][128], out [Hq][128].  Attends to positions
+ * 0 .. d_pos[0] (s_kv = d_pos[0]+1, clamped to max_ctx).  num_splits <= 0
+ * picks grout_attn_decode_default_splits(max_ctx, ...).
+ * Replaces fmha_decode_gqa_split + splitk_reduce_merge
+ * (src/kernels.rs:3996-4304) as recorded in src/model.rs:3713-3771. */
+int grout_attn_decode(const void* q, const void* k_cache, const void* v_cache, void* out,
+                      void* workspace, size_t workspace_bytes, const uint32_t* d_pos,
+                      int num_q_heads, int num_kv_heads, int head_dim, int max_ctx,
+                      long kv_head_stride, int num_splits, float qk_scale, void* stream);
+
+/* The two halves of grout_attn_decode, for callers that schedule them
+ * separately (the reference records them as two kernels).  part_acc
+ * [Hkv][splits][G][128] fp32 unnormalized, part_ml [Hkv][splits][G][2] fp32
+ * (running max in log2 units, sum of 2^(s - max)). */
+int grout_fmha_decode_gqa_split(const void* q, const void* k_cache, const void* v_cache,
+                                float* part_acc, float* part_ml, const uint32_t* d_pos,
+                                int num_q_heads, int num_kv_heads, int head_dim, int max_ctx,
+                                long kv_head_stride, int num_splits, float qk_scale,
+                                void* stream);
+int grout_splitk_reduce_merge(const float* part_acc, const float* part_ml, void* out,
+                              int num_q_heads, int num_kv_heads, int head_dim, int num_splits,
+                              void* stream);
+
+/* ------------------------------------------------------------------ */
+/* Decode-step graph (a8)                                              */
+/* ------------------------------------------------------------------ */
+
+/* Per-layer buffers of the attention part of one decode step. */
+typedef struct grout_decode_layer {
+  const void* qkv;      /* [(Hq+2Hkv)*128] fp16 input of the fused norm/RoPE/KV write */
+  const void* gamma_q;  /* [128] fp16 */
+  const void* gamma_k;  /* [128] fp16 */
+  void* q_rope;         /* [Hq][128] fp16 scratch: rotated q */
+  void* k_cache;        /* [Hkv][max_ctx][128] fp16 */
+  void* v_cache;        /* [Hkv][max_ctx][128] fp16 */
+  void* attn_out;       /* [Hq][128] fp16 */
+} grout_decode_layer;
+
+typedef struct grout_decode_graph grout_decode_graph;
+
+/* Captures, on `stream`, num_layers x [fused norm/RoPE/KV write -> split-K
+ * decode -> merge] into one HIP graph.  The graph reads the position from
+ * its own device word, written by grout_decode_graph_launch; `workspace`
+ * (grout_attn_decode_workspace_bytes(..., num_splits)) is shared by the
+ * layers, which run in order.  num_splits <= 0 picks the default for max_ctx.
+ * Replaces DecodeCudaGraphRunner / build_decode_graph_scope
+ * (src/model.rs:408-596, 2631-4006) for the attention records. */
+int grout_decode_graph_create(const grout_decode_layer* layers, int num_layers,
+                              const float* rope_cos, const float* rope_sin, void* workspace,
+                              size_t workspace_bytes, int num_q_heads, int num_kv_heads,
+                              int head_dim, int max_ctx, int num_splits, float eps,
+                              float qk_scale, void* stream, grout_decode_graph** out);
+
+/* Uploads `position` (host-checked: position < max_ctx) into the graph's
+ * device word and launches the graph on `stream`; asynchronous.
+ * Mirrors DecodeCudaGraphRunner::launch_step (src/model.rs:466-506). */
+int grout_decode_graph_launch(grout_decode_graph* graph, uint32_t position, void* stream);
+
+/* Device address of the graph's position word (u32), for callers that chain
+ * their own kernels on it. */
+const uint32_t* grout_decode_graph_position_ptr(const grout_decode_graph* graph);
+
+int grout_decode_graph_destroy(grout_decode_graph* graph);
+
+/* ------------------------------------------------------------------ */
+/* Diagnostics                                                         */
+/* ------------------------------------------------------------------ */
+
+/* Runs one v_mfma_f32_16x16x32_f16 with A[l][i] = 8l+i and a 0/1 selector B,
+ * writing the 64x4 C fragment to out (device, 256 floats).  Confirms the
+ * operand/accumulator lane layout every kernel here assumes. */
+int grout_diag_mfma_layout(float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GROUT_ATTN_H */

@@ -1,0 +1,478 @@
+/*
+ * grout_oracle.c -- CPU restatement of grout's attention hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker, never the product:
+ * only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+ * load it.  The product (grout_amd/libgrout_attn.so) neither links nor calls
+ * anything here, and fails loudly when its HIP code is missing.
+ *
+ * Scalar fp32 arithmetic over fp16 storage (uint16_t bit patterns), written
+ * from the reference's algorithm (rtburger/grout, Rust + cuTile):
+ *
+ *   go_inv_freq            src/model.rs:7295-7306   (build_inv_freq)
+ *   go_rope_table          src/kernels.rs:5076-5082 (theta = pos*inv_freq; cos/sin),
+ *                          src/kernels.rs:1768-1786 (NeoX half-split layout)
+ *   go_qk_norm_rope_row    src/kernels.rs:4999-5088 (x*rsqrt(ss/D+eps)*gamma, rotate)
+ *   go_qk_norm_rope_kv_prefill  src/kernels.rs:4837-5168
+ *   go_qk_norm_rope_kv_decode   src/kernels.rs:5170-5452
+ *   go_attention_prefill_rows   src/kernels.rs:2576-2725 (causal, q_pos = pos0+row,
+ *                               k_pos <= q_pos), loop structure of
+ *                               benchmarks/src/bin/attention_microbench.rs:665-702
+ *   go_attention_decode         src/kernels.rs:4022-4185 with s_kv = pos+1
+ *   go_decode_split, go_splitk_merge  src/kernels.rs:4022-4185, 4207-4304
+ *                               (tiles_per_split = ceil(ceil(s_kv/BN)/NKS),
+ *                               log2-domain LSE, weights 2^(lse-max)/sum)
+ *
+ * Cache layout everywhere: [Hkv][max_ctx][D] (src/model.rs:1587-1592), with an
+ * explicit kv_head_stride in elements (max_ctx*D for the engine's caches).
+ *
+ * Bit-exactness contract for the fused norm/RoPE/KV write: the sum of squares
+ * uses a fixed tree (32 lanes x 4 elements, xor butterfly 16,8,4,2,1), the
+ * reciprocal square root is a fixed double-precision Newton sequence, and no
+ * multiply-add is contracted (build with -ffp-contract=off).  The HIP kernel
+ * performs the identical sequence of IEEE operations, so K-cache rows match
+ * bit for bit.  The reference's own reduction order (cuTile reduce_sum) is
+ * unspecified; the math is the same.
+ *
+ * Deliberate deviations from the reference, each a defect or a rounding
+ * detail of the reference rather than its intended math:
+ *   - decode qk_scale is 1/sqrt(D) in fp32 (the reference rounds it to f16,
+ *     src/model.rs:3725);
+ *   - split partials stay fp32 (the reference rounds them to f16,
+ *     src/kernels.rs:4176-4179), and P is not rounded to f16 before P.V.
+ */
+#include <math.h>
+#include <pthread.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------ */
+/* fp16 <-> fp32                                                      */
+/* ------------------------------------------------------------------ */
+
+float go_h2f(uint16_t h) {
+  uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu, x;
+  float f;
+  if (e == 0) {
+    f = (float)m * 5.9604644775390625e-08f; /* m * 2^-24, exact */
+    memcpy(&x, &f, 4);
+    x |= sign;
+  } else if (e == 31) {
+    x = sign | 0x7f800000u | (m << 13);
+  } else {
+    x = sign | ((e + 112u) << 23) | (m << 13);
+  }
+  memcpy(&f, &x, 4);
+  return f;
+}
+
+/* fp32 -> fp16, round to nearest even (the GPU's v_cvt_f16_f32 default). */
+uint16_t go_f2h(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  uint32_t sign = (x >> 16) & 0x8000u;
+  uint32_t ax = x & 0x7fffffffu;
+  if (ax >= 0x7f800000u) /* inf / nan */
+    return (uint16_t)(sign | 0x7c00u | (ax > 0x7f800000u ? (0x200u | ((ax >> 13) & 0x3ffu)) : 0u));
+  if (ax >= 0x477ff000u) /* >= 65520 rounds to inf */
+    return (uint16_t)(sign | 0x7c00u);
+  if (ax >= 0x38800000u) { /* normal half */
+    ax += 0xfffu + ((ax >> 13) & 1u);
+    ax -= 0x38000000u;
+    return (uint16_t)(sign | (ax >> 13));
+  }
+  /* half subnormal or zero: round |f| * 2^24 to the nearest even integer */
+  float a;
+  memcpy(&a, &ax, 4);
+  uint32_t m = (uint32_t)rintf(a * 16777216.0f);
+  return (uint16_t)(sign | m);
+}
+
+/* double -> fp16 rounded once: round-to-odd into fp32 (24 >= 11+2 bits), then RNE. */
+static uint16_t go_d2h(double d) {
+  if (!(fabs(d) >= 1e-30)) return go_f2h((float)d); /* zero / far below half range */
+  float f = (float)d;
+  if ((double)f != d && !isinf(f)) {
+    uint32_t b;
+    memcpy(&b, &f, 4);
+    if (fabs((double)f) > fabs(d)) b -= 1u; /* step toward zero */
+    b |= 1u;
+    memcpy(&f, &b, 4);
+  }
+  return go_f2h(f);
+}
+
+void go_h2f_array(const uint16_t* in, float* out, size_t n) {
+  for (size_t i = 0; i < n; ++i) out[i] = go_h2f(in[i]);
+}
+void go_f2h_array(const float* in, uint16_t* out, size_t n) {
+  for (size_t i = 0; i < n; ++i) out[i] = go_f2h(in[i]);
+}
+
+/* ------------------------------------------------------------------ */
+/* Seeded inputs: SplitMix64 -> Box-Muller in f64 -> f16 (RNE, once)   */
+/* ------------------------------------------------------------------ */
+
+static uint64_t go_mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ULL;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebULL;
+  return z ^ (z >> 31);
+}
+/* k-th output (k >= 1) of SplitMix64 seeded with `seed`. */
+static uint64_t go_sm64_at(uint64_t seed, uint64_t k) {
+  return go_mix64(seed + k * 0x9e3779b97f4a7c15ULL);
+}
+/* uniform in the open interval (0, 1) */
+static double go_u01(uint64_t r) { return ((double)(r >> 11) + 0.5) * 0x1.0p-53; }
+
+uint64_t go_splitmix64_at(uint64_t seed, uint64_t k) { return go_sm64_at(seed, k); }
+
+/* Element i of the N(0,1) stream: pair p = i/2 uses draws 2p+1 (radius) and
+ * 2p+2 (angle); even i takes the cosine branch, odd i the sine branch. */
+static double go_normal_at(uint64_t seed, uint64_t i) {
+  uint64_t p = i >> 1;
+  double u1 = go_u01(go_sm64_at(seed, 2 * p + 1));
+  double u2 = go_u01(go_sm64_at(seed, 2 * p + 2));
+  double r = sqrt(-2.0 * log(u1));
+  double a = 6.283185307179586476925286766559 * u2;
+  return (i & 1) ? r * sin(a) : r * cos(a);
+}
+
+void go_fill_normal_f16(uint64_t seed, size_t n, uint16_t* out) {
+  for (size_t i = 0; i < n; ++i) out[i] = go_d2h(go_normal_at(seed, i));
+}
+void go_fill_normal_f64(uint64_t seed, size_t n, double* out) {
+  for (size_t i = 0; i < n; ++i) out[i] = go_normal_at(seed, i);
+}
+void go_fill_uniform_f16(uint64_t seed, double lo, double hi, size_t n, uint16_t* out) {
+  for (size_t i = 0; i < n; ++i) out[i] = go_d2h(lo + (hi - lo) * go_u01(go_sm64_at(seed, i + 1)));
+}
+
+/* ------------------------------------------------------------------ */
+/* RoPE tables (a9)                                                   */
+/* ------------------------------------------------------------------ */
+
+/* src/model.rs:7295-7306: inv_freq[i/2] = 1 / theta^(i/D), i = 0,2,..,D-2, in f32. */
+void go_inv_freq(int D, float theta, float* inv_freq) {
+  for (int i = 0; i < D; i += 2) {
+    float p = (float)i / (float)D;
+    inv_freq[i / 2] = 1.0f / powf(theta, p);
+  }
+}
+
+/* cos/sin[pos][i] of the f32 angle (float)pos * inv_freq[i] (src/kernels.rs:5076-5082),
+ * evaluated in double and rounded once to f32. Layout [max_ctx][D/2]. */
+void go_rope_table(int max_ctx, int D, float theta, float* cos_t, float* sin_t) {
+  int half = D / 2;
+  float* inv = (float*)malloc(sizeof(float) * (size_t)half);
+  go_inv_freq(D, theta, inv);
+  for (int p = 0; p < max_ctx; ++p) {
+    float pf = (float)p;
+    for (int i = 0; i < half; ++i) {
+      float ang = pf * inv[i];
+      cos_t[(size_t)p * half + i] = (float)cos((double)ang);
+      sin_t[(size_t)p * half + i] = (float)sin((double)ang);
+    }
+  }
+  free(inv);
+}
+
+/* ------------------------------------------------------------------ */
+/* Fused QK-RMSNorm + RoPE (+ KV write)  (a1, a2)                      */
+/* ------------------------------------------------------------------ */
+
+/* 1/sqrt(v): bit-trick seed, four Newton steps in double, one rounding to f32.
+ * Only IEEE mul/sub/convert: identical on any conforming CPU or GPU. */
+float go_rsqrt_det(float v) {
+  uint32_t b;
+  memcpy(&b, &v, 4);
+  b = 0x5f3759dfu - (b >> 1);
+  float y0;
+  memcpy(&y0, &b, 4);
+  double y = (double)y0, vd = (double)v;
+  for (int it = 0; it < 4; ++it) {
+    double t = vd * y;
+    t = t * y;
+    t = 0.5 * t;
+    t = 1.5 - t;
+    y = y * t;
+  }
+  return (float)y;
+}
+
+/* Sum of squares of a D=128 row with the kernel's tree: lane j (0..31) owns
+ * elements 4j..4j+3 and forms (x0^2+x1^2)+(x2^2+x3^2); the 32 lane values are
+ * combined by an xor butterfly at distances 16, 8, 4, 2, 1. */
+float go_sumsq_row128(const uint16_t* x) {
+  float p[32], t[32];
+  for (int j = 0; j < 32; ++j) {
+    float a = go_h2f(x[4 * j + 0]), b = go_h2f(x[4 * j + 1]);
+    float c = go_h2f(x[4 * j + 2]), d = go_h2f(x[4 * j + 3]);
+    float ab = a * a, bb = b * b, cc = c * c, dd = d * d;
+    float s0 = ab + bb, s1 = cc + dd;
+    p[j] = s0 + s1;
+  }
+  for (int off = 16; off >= 1; off >>= 1) {
+    for (int j = 0; j < 32; ++j) t[j] = p[j] + p[j ^ off];
+    memcpy(p, t, sizeof(p));
+  }
+  return p[0];
+}
+
+/* One head row: out = f16(rotate(x * inv_rms * gamma)), NeoX halves [0,D/2) and
+ * [D/2,D): y_lo = n_lo*c - n_hi*s, y_hi = n_hi*c + n_lo*s. D must be 128. */
+void go_qk_norm_rope_row(const uint16_t* x, const uint16_t* gamma, const float* cos_row,
+                         const float* sin_row, float eps, uint16_t* out) {
+  const int D = 128, H = 64;
+  float ss = go_sumsq_row128(x);
+  float mean = ss / (float)D;
+  float v = mean + eps;
+  float inv = go_rsqrt_det(v);
+  for (int i = 0; i < H; ++i) {
+    float xl = go_h2f(x[i]), xh = go_h2f(x[i + H]);
+    float gl = go_h2f(gamma[i]), gh = go_h2f(gamma[i + H]);
+    float nl = xl * inv;
+    nl = nl * gl;
+    float nh = xh * inv;
+    nh = nh * gh;
+    float c = cos_row[i], s = sin_row[i];
+    float a = nl * c, b = nh * s;
+    float yl = a - b;
+    float e = nh * c, f = nl * s;
+    float yh = e + f;
+    out[i] = go_f2h(yl);
+    out[i + H] = go_f2h(yh);
+  }
+}
+
+/* Prefill (src/kernels.rs:4837-5168): q[S][Hq][D], k,v[S][Hkv][D] ->
+ * q_out[S][Hq][D], k_cache/v_cache[kvh][pos0+s][D] (head stride in elements). */
+void go_qk_norm_rope_kv_prefill(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                const uint16_t* gamma_q, const uint16_t* gamma_k,
+                                const float* cos_t, const float* sin_t, uint16_t* q_out,
+                                uint16_t* k_cache, uint16_t* v_cache, int pos0, int S, int Hq,
+                                int Hkv, int D, long kv_head_stride, float eps) {
+  int half = D / 2;
+  for (int s = 0; s < S; ++s) {
+    int pos = pos0 + s;
+    const float* c = cos_t + (size_t)pos * half;
+    const float* sn = sin_t + (size_t)pos * half;
+    for (int h = 0; h < Hq; ++h) {
+      size_t off = ((size_t)s * Hq + h) * D;
+      go_qk_norm_rope_row(q + off, gamma_q, c, sn, eps, q_out + off);
+    }
+    for (int h = 0; h < Hkv; ++h) {
+      size_t in_off = ((size_t)s * Hkv + h) * D;
+      size_t c_off = (size_t)h * kv_head_stride + (size_t)pos * D;
+      go_qk_norm_rope_row(k + in_off, gamma_k, c, sn, eps, k_cache + c_off);
+      memcpy(v_cache + c_off, v + in_off, sizeof(uint16_t) * (size_t)D);
+    }
+  }
+}
+
+/* Decode (src/kernels.rs:5170-5452): qkv = [Q(Hq*D) | K(Hkv*D) | V(Hkv*D)] at `pos`. */
+void go_qk_norm_rope_kv_decode(const uint16_t* qkv, const uint16_t* gamma_q,
+                               const uint16_t* gamma_k, const float* cos_t, const float* sin_t,
+                               uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, int pos,
+                               int Hq, int Hkv, int D, long kv_head_stride, float eps) {
+  const uint16_t* q = qkv;
+  const uint16_t* k = qkv + (size_t)Hq * D;
+  const uint16_t* v = k + (size_t)Hkv * D;
+  go_qk_norm_rope_kv_prefill(q, k, v, gamma_q, gamma_k, cos_t, sin_t, q_out, k_cache, v_cache,
+                             pos, 1, Hq, Hkv, D, kv_head_stride, eps);
+}
+
+/* ------------------------------------------------------------------ */
+/* Attention (a3..a6)                                                  */
+/* ------------------------------------------------------------------ */
+
+/* One query row against kv positions [0, n_kv): fp32 scores, exact softmax
+ * (max-subtracted expf), fp32 output.  Loop order of attention_microbench.rs:665-702. */
+static void go_attend_row(const float* qrow, const uint16_t* kh, const uint16_t* vh, int n_kv,
+                          int D, float scale, float* scores, float* out) {
+  float mx = -INFINITY;
+  for (int n = 0; n < n_kv; ++n) {
+    const uint16_t* kr = kh + (size_t)n * D;
+    float dot = 0.0f;
+    for (int d = 0; d < D; ++d) dot += qrow[d] * go_h2f(kr[d]);
+    float sc = dot * scale;
+    scores[n] = sc;
+    if (sc > mx) mx = sc;
+  }
+  float den = 0.0f;
+  for (int n = 0; n < n_kv; ++n) {
+    scores[n] = expf(scores[n] - mx);
+    den += scores[n];
+  }
+  for (int d = 0; d < D; ++d) out[d] = 0.0f;
+  for (int n = 0; n < n_kv; ++n) {
+    float w = scores[n] / den;
+    const uint16_t* vr = vh + (size_t)n * D;
+    for (int d = 0; d < D; ++d) out[d] += w * go_h2f(vr[d]);
+  }
+}
+
+/* Causal GQA prefill for selected rows: q[S][Hq][D] (post-RoPE), caches
+ * [Hkv][..][D] with head stride, out[nrows][Hq][D] fp32.  Row r attends to
+ * kv positions 0..pos0+r; kvh = h / (Hq/Hkv). */
+typedef struct {
+  const uint16_t *q, *kc, *vc;
+  float* out;
+  const int* rows;
+  int nrows, S, pos0, Hq, Hkv, D, h0, h1;
+  long hs;
+  float scale;
+} go_prefill_job;
+
+static void* go_prefill_worker(void* arg) {
+  go_prefill_job* j = (go_prefill_job*)arg;
+  int G = j->Hq / j->Hkv, D = j->D;
+  float* qrow = (float*)malloc(sizeof(float) * (size_t)D);
+  float* scores = (float*)malloc(sizeof(float) * (size_t)(j->pos0 + j->S));
+  for (int ri = 0; ri < j->nrows; ++ri) {
+    int r = j->rows[ri];
+    for (int h = j->h0; h < j->h1; ++h) {
+      const uint16_t* qs = j->q + ((size_t)r * j->Hq + h) * D;
+      for (int d = 0; d < D; ++d) qrow[d] = go_h2f(qs[d]);
+      int kvh = h / G;
+      go_attend_row(qrow, j->kc + (size_t)kvh * j->hs, j->vc + (size_t)kvh * j->hs,
+                    j->pos0 + r + 1, D, j->scale, scores,
+                    j->out + ((size_t)ri * j->Hq + h) * D);
+    }
+  }
+  free(qrow);
+  free(scores);
+  return NULL;
+}
+
+void go_attention_prefill_rows(const uint16_t* q, const uint16_t* k_cache,
+                               const uint16_t* v_cache, float* out, const int* rows, int nrows,
+                               int S, int pos0, int Hq, int Hkv, int D, long kv_head_stride,
+                               float scale, int nthreads) {
+  if (nthreads < 1) nthreads = 1;
+  if (nthreads > Hq) nthreads = Hq;
+  pthread_t th[256];
+  go_prefill_job jobs[256];
+  if (nthreads > 256) nthreads = 256;
+  for (int t = 0; t < nthreads; ++t) {
+    go_prefill_job j = {q, k_cache, v_cache, out, rows, nrows, S, pos0, Hq, Hkv, D,
+                        (Hq * t) / nthreads, (Hq * (t + 1)) / nthreads, kv_head_stride, scale};
+    jobs[t] = j;
+  }
+  if (nthreads == 1) {
+    go_prefill_worker(&jobs[0]);
+    return;
+  }
+  for (int t = 0; t < nthreads; ++t) pthread_create(&th[t], NULL, go_prefill_worker, &jobs[t]);
+  for (int t = 0; t < nthreads; ++t) pthread_join(th[t], NULL);
+}
+
+/* Decode: q[Hq][D] (post-RoPE) against s_kv = pos+1 cached positions; out[Hq][D] fp32. */
+void go_attention_decode(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                         float* out, int pos, int Hq, int Hkv, int D, long kv_head_stride,
+                         float scale, int nthreads) {
+  int row0 = 0;
+  /* decode == one prefill row at absolute position pos (S=1, pos0=pos) */
+  go_attention_prefill_rows(q, k_cache, v_cache, out, &row0, 1, 1, pos, Hq, Hkv, D,
+                            kv_head_stride, scale, nthreads);
+}
+
+/* Split-K decode (src/kernels.rs:4022-4185): per (kvh, split) the online
+ * softmax in log2 units over tiles [split*tps, min((split+1)*tps, tiles)),
+ * tiles = ceil(s_kv/BN), tps = ceil(tiles/NKS).  Emits the normalized partial
+ * att[kvh][split*G+g][D] and lse[kvh][split*G+g] = m + log2(max(l,1e-8)).
+ * An empty split keeps the reference's l init of BN ones (so lse ~ -1e30). */
+void go_decode_split(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                     float* att, float* lse, int pos, int Hq, int Hkv, int D,
+                     long kv_head_stride, float scale, int BN, int NKS) {
+  int G = Hq / Hkv;
+  int s_kv = pos + 1;
+  int tiles = (s_kv + BN - 1) / BN;
+  int tps = (tiles + NKS - 1) / NKS;
+  float scale_log2 = scale / logf(2.0f);
+  float* qf = (float*)malloc(sizeof(float) * (size_t)D);
+  float* acc = (float*)malloc(sizeof(float) * (size_t)D);
+  float* sc = (float*)malloc(sizeof(float) * (size_t)BN);
+  for (int kvh = 0; kvh < Hkv; ++kvh) {
+    const uint16_t* kh = k_cache + (size_t)kvh * kv_head_stride;
+    const uint16_t* vh = v_cache + (size_t)kvh * kv_head_stride;
+    for (int sp = 0; sp < NKS; ++sp) {
+      int t0 = sp * tps, t1 = t0 + tps < tiles ? t0 + tps : tiles;
+      for (int g = 0; g < G; ++g) {
+        const uint16_t* qs = q + ((size_t)kvh * G + g) * D;
+        for (int d = 0; d < D; ++d) qf[d] = go_h2f(qs[d]);
+        float m = -1.0e30f, l = (t0 < t1) ? 0.0f : (float)BN;
+        for (int d = 0; d < D; ++d) acc[d] = 0.0f;
+        for (int t = t0; t < t1; ++t) {
+          float tmax = -1.0e30f;
+          for (int n = 0; n < BN; ++n) {
+            int p = t * BN + n;
+            float s = -1.0e30f;
+            if (p < s_kv) {
+              const uint16_t* kr = kh + (size_t)p * D;
+              float dot = 0.0f;
+              for (int d = 0; d < D; ++d) dot += qf[d] * go_h2f(kr[d]);
+              s = dot * scale_log2;
+            }
+            sc[n] = s;
+            if (s > tmax) tmax = s;
+          }
+          float mn = m > tmax ? m : tmax;
+          float alpha = exp2f(m - mn);
+          float lsum = 0.0f;
+          for (int d = 0; d < D; ++d) acc[d] *= alpha;
+          for (int n = 0; n < BN; ++n) {
+            int p = t * BN + n;
+            float pr = (p < s_kv) ? exp2f(sc[n] - mn) : 0.0f;
+            lsum += pr;
+            if (pr != 0.0f) {
+              const uint16_t* vr = vh + (size_t)p * D;
+              for (int d = 0; d < D; ++d) acc[d] += pr * go_h2f(vr[d]);
+            }
+          }
+          l = l * alpha + lsum;
+          m = mn;
+        }
+        float ls = l > 1.0e-8f ? l : 1.0e-8f;
+        size_t row = (size_t)kvh * NKS * G + (size_t)sp * G + g;
+        for (int d = 0; d < D; ++d) att[row * D + d] = acc[d] / ls;
+        lse[row] = m + log2f(ls);
+      }
+    }
+  }
+  free(qf);
+  free(acc);
+  free(sc);
+}
+
+/* Merge (src/kernels.rs:4207-4304): w_s = 2^(lse_s - max) / max(sum, 1e-8);
+ * out[kvh*G+g][d] = sum_s w_s * att[kvh][s*G+g][d]. */
+void go_splitk_merge(const float* att, const float* lse, float* out, int Hq, int Hkv, int D,
+                     int NKS) {
+  int G = Hq / Hkv;
+  float* w = (float*)malloc(sizeof(float) * (size_t)NKS);
+  for (int kvh = 0; kvh < Hkv; ++kvh) {
+    for (int g = 0; g < G; ++g) {
+      float mx = -INFINITY;
+      for (int s = 0; s < NKS; ++s) {
+        float v = lse[(size_t)kvh * NKS * G + (size_t)s * G + g];
+        if (v > mx) mx = v;
+      }
+      float sum = 0.0f;
+      for (int s = 0; s < NKS; ++s) {
+        w[s] = exp2f(lse[(size_t)kvh * NKS * G + (size_t)s * G + g] - mx);
+        sum += w[s];
+      }
+      float den = sum > 1.0e-8f ? sum : 1.0e-8f;
+      for (int d = 0; d < D; ++d) {
+        float o = 0.0f;
+        for (int s = 0; s < NKS; ++s)
+          o += (w[s] / den) * att[((size_t)kvh * NKS * G + (size_t)s * G + g) * D + d];
+        out[((size_t)kvh * G + g) * D + d] = o;
+      }
+    }
+  }
+  free(w);
+}

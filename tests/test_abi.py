@@ -1,0 +1,120 @@
+"""CPU checks of the C ABI boundary: the library loads, exports every symbol
+include/grout_attn.h declares, and rejects bad arguments before touching a GPU."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+import grout_amd
+from grout_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "grout_attn.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"\b(grout_[a-z0-9_]+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_library_is_built_and_loads():
+    assert os.path.exists(grout_amd.LIB_PATH), "run `python -m grout_amd.build` first"
+    L = grout_amd.lib()
+    assert L.grout_abi_version() >> 16 == 1
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    names = header_functions()
+    assert len(names) >= 17
+    L = grout_amd.lib()
+    for n in names:
+        assert hasattr(L, n), f"{n} declared in grout_attn.h but not exported"
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(names)
+
+
+def test_rope_host_functions_match_oracle_bit_for_bit():
+    import oracle as O
+
+    inv = np.empty(64, np.float32)
+    assert grout_amd.lib().grout_rope_inv_freq(128, 1e6, inv.ctypes.data_as(C.c_void_p)) == 0
+    assert np.array_equal(inv, O.inv_freq(128, 1e6))
+    c = np.empty((300, 64), np.float32)
+    s = np.empty((300, 64), np.float32)
+    assert grout_amd.lib().grout_rope_table_host(300, 128, 1e6, c.ctypes.data_as(C.c_void_p),
+                                                 s.ctypes.data_as(C.c_void_p)) == 0
+    oc, os_ = O.rope_table(300, 128, 1e6)
+    assert np.array_equal(c, oc) and np.array_equal(s, os_)
+
+
+def _aligned(n=4096):
+    buf = (C.c_char * (n + 64))()
+    addr = (C.addressof(buf) + 63) & ~63
+    return buf, C.c_void_p(addr)
+
+
+def test_argument_validation_without_gpu():
+    L = grout_amd.lib()
+    keep, p = _aligned()
+    # head_dim != 128 -> not supported
+    rc = L.grout_fmha_prefill(p, p, p, p, 16, 0, 8, 2, 64, 16 * 64, 0.125, None)
+    assert rc == -3 and "head_dim" in _lib.last_error()
+    # Hq not a multiple of Hkv
+    rc = L.grout_fmha_prefill(p, p, p, p, 16, 0, 6, 4, 128, 16 * 128, 0.088, None)
+    assert rc == -1 and "multiple" in _lib.last_error()
+    # empty prefill
+    rc = L.grout_fmha_prefill(p, p, p, p, 0, 0, 8, 2, 128, 16 * 128, 0.088, None)
+    assert rc == -1
+    # misaligned pointer
+    bad = C.c_void_p(p.value + 2)
+    rc = L.grout_fmha_prefill(bad, p, p, p, 4, 0, 8, 2, 128, 16 * 128, 0.088, None)
+    assert rc == -2 and "aligned" in _lib.last_error()
+    # kv head stride too small for pos0 + seq_len rows
+    rc = L.grout_fmha_prefill(p, p, p, p, 8, 10, 8, 2, 128, 16 * 128, 0.088, None)
+    assert rc == -1 and "kv_head_stride" in _lib.last_error()
+    # fused write out of cache range
+    rc = L.grout_qk_norm_rope_kv_prefill(p, p, p, p, p, p, p, p, p, p, 30, 8, 8, 2, 128, 32,
+                                         32 * 128, 1e-6, None)
+    assert rc == -1 and "exceeds max_seq_len" in _lib.last_error()
+    # decode group above 16
+    rc = L.grout_attn_decode(p, p, p, p, p, 1 << 20, p, 34, 2, 128, 64, 64 * 128, 4, 0.088, None)
+    assert rc == -3
+    # workspace too small
+    rc = L.grout_attn_decode(p, p, p, p, p, 16, p, 8, 2, 128, 64, 64 * 128, 4, 0.088, None)
+    assert rc == -1 and "workspace" in _lib.last_error()
+    # NULL position pointer
+    rc = L.grout_fmha_decode_gqa_split(p, p, p, p, p, None, 8, 2, 128, 64, 64 * 128, 2, 0.088, None)
+    assert rc == -1 and "d_pos" in _lib.last_error()
+
+
+def test_decode_split_defaults_and_workspace():
+    L = grout_amd.lib()
+    assert L.grout_attn_decode_default_splits(1, 32, 8) == 1
+    assert L.grout_attn_decode_default_splits(4096, 32, 8) == 16
+    assert L.grout_attn_decode_default_splits(32768, 64, 8) == 64
+    ws = L.grout_attn_decode_workspace_bytes(64, 8, 128, 64)
+    assert ws == 8 * 64 * 8 * 130 * 4
+    assert L.grout_attn_decode_workspace_bytes(64, 8, 96, 64) == 0
+
+
+def test_graph_create_rejects_bad_layers_without_gpu():
+    L = grout_amd.lib()
+    layers = (_lib.DecodeLayer * 1)()
+    h = C.c_void_p()
+    keep, p = _aligned()
+    rc = L.grout_decode_graph_create(layers, 1, p, p, p, 1 << 20, 32, 8, 128, 4096, 0, 1e-6, 0.088,
+                                     None, C.byref(h))
+    assert rc == -1 and "layer 0" in _lib.last_error()
+    assert L.grout_decode_graph_launch(None, 0, None) == -1
+    assert L.grout_decode_graph_destroy(None) == 0
+
+
+def test_ops_fail_loudly_without_library(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "missing.so"))
+    with pytest.raises(RuntimeError, match="missing"):
+        _lib.lib()

@@ -1,0 +1,263 @@
+"""GPU parity of the gfx950 kernels (through the C ABI) against the CPU oracle.
+
+Inputs come from the oracle's seeded SplitMix64/Box-Muller generator.  Bars:
+K/V cache rows and indexing bit-exact; attention outputs within max-abs 1e-2
+and mean-abs 1e-3 of the fp32 oracle."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_util import D, assert_close, dev, gamma, host, host_f32, normal
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print("[case]", *a, flush=True)
+
+
+# ------------------------------------------------------------------ layout
+
+
+def test_mfma_layout_probe(gpu):
+    out = gpu.ops.diag_mfma_layout().cpu().numpy()
+    for l in range(64):
+        for j in range(4):
+            m, n = 4 * (l // 16) + j, l % 16  # C fragment: col l%16, rows 4*(l/16)+j
+            # A row m, k-slot n//8 is held by lane m + 16*(n//8) at element n%8
+            assert out[l, j] == (m + 16 * (n // 8)) * 8 + n % 8, (l, j, out[l, j])
+
+
+# ------------------------------------------------- fused norm / RoPE / KV write
+
+
+@pytest.mark.parametrize("S,Hq,Hkv,pos0,max_ctx", [
+    (1, 16, 8, 0, 64), (37, 32, 8, 100, 256), (64, 40, 8, 5, 128), (2048, 32, 8, 0, 32768)])
+def test_qk_norm_rope_kv_prefill_bit_exact(gpu, S, Hq, Hkv, pos0, max_ctx):
+    _say("norm_rope_prefill", S, Hq, Hkv, pos0, max_ctx)
+    q, k, v = normal("nq", (S, Hq, D)), normal("nk", (S, Hkv, D)), normal("nv", (S, Hkv, D))
+    gq, gk = gamma("gq"), gamma("gk")
+    cos, sin = O.rope_table(max_ctx, D, 1e6)
+    kc = np.full((Hkv, max_ctx, D), 0x7BFF, np.uint16)  # canary in every slot
+    vc = kc.copy()
+    kc_ref, vc_ref = kc.copy(), vc.copy()
+    q_ref = O.qk_norm_rope_kv_prefill(q, k, v, gq, gk, cos, sin, kc_ref, vc_ref, pos0, 1e-6)
+
+    rope = gpu.ops.rope_tables(max_ctx)
+    kc_d, vc_d = dev(kc), dev(vc)
+    q_out = gpu.ops.qk_norm_rope_kv_prefill(dev(q), dev(k), dev(v), dev(gq), dev(gk), rope, kc_d,
+                                            vc_d, pos0)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(q_out), q_ref), "rotated q differs"
+    assert np.array_equal(host(kc_d), kc_ref), "k cache differs (incl. untouched canary slots)"
+    assert np.array_equal(host(vc_d), vc_ref), "v cache differs (incl. untouched canary slots)"
+
+
+@pytest.mark.parametrize("Hq,Hkv,pos,max_ctx", [(16, 8, 512, 1024), (64, 8, 32767, 32768), (32, 8, 0, 64)])
+def test_qk_norm_rope_kv_decode_bit_exact(gpu, Hq, Hkv, pos, max_ctx):
+    _say("norm_rope_decode", Hq, Hkv, pos, max_ctx)
+    qkv = normal("dqkv", ((Hq + 2 * Hkv) * D,))
+    gq, gk = gamma("gq"), gamma("gk")
+    cos, sin = O.rope_table(max_ctx, D, 1e6)
+    kc = normal("dkc", (Hkv, max_ctx, D))
+    vc = normal("dvc", (Hkv, max_ctx, D))
+    kc_ref, vc_ref = kc.copy(), vc.copy()
+    q_ref = O.qk_norm_rope_kv_decode(qkv, gq, gk, cos, sin, kc_ref, vc_ref, pos, Hq, Hkv, 1e-6)
+    rope = gpu.ops.rope_tables(max_ctx)
+    kc_d, vc_d = dev(kc), dev(vc)
+    p = torch.tensor([pos], dtype=torch.int32, device="cuda")
+    q_out = gpu.ops.qk_norm_rope_kv_decode(dev(qkv), dev(gq), dev(gk), rope, kc_d, vc_d, p, Hq)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(q_out), q_ref)
+    assert np.array_equal(host(kc_d), kc_ref)
+    assert np.array_equal(host(vc_d), vc_ref)
+
+
+def test_qk_norm_rope_kv_decode_out_of_range_position_writes_nothing(gpu):
+    Hq, Hkv, max_ctx = 16, 8, 64
+    qkv = normal("oqkv", ((Hq + 2 * Hkv) * D,))
+    rope = gpu.ops.rope_tables(max_ctx)
+    kc_d = torch.zeros((Hkv, max_ctx, D), dtype=torch.float16, device="cuda")
+    vc_d = torch.zeros_like(kc_d)
+    p = torch.tensor([max_ctx], dtype=torch.int32, device="cuda")
+    gq = dev(gamma("gq"))
+    gpu.ops.qk_norm_rope_kv_decode(dev(qkv), gq, gq, rope, kc_d, vc_d, p, Hq)
+    torch.cuda.synchronize()
+    assert int(torch.count_nonzero(kc_d)) == 0 and int(torch.count_nonzero(vc_d)) == 0
+
+
+# ------------------------------------------------------------ decode attention
+
+
+def _decode_case(gpu, Hq, Hkv, ctx, max_ctx, num_splits, tag):
+    _say("decode", Hq, Hkv, ctx, max_ctx, num_splits)
+    q = normal(tag + "q", (Hq, D))
+    kc = normal(tag + "k", (Hkv, max_ctx, D))
+    vc = normal(tag + "v", (Hkv, max_ctx, D))
+    ref = O.attention_decode(q, kc, vc, ctx - 1, nthreads=8)
+    p = torch.tensor([ctx - 1], dtype=torch.int32, device="cuda")
+    out = gpu.ops.attn_decode(dev(q), dev(kc), dev(vc), p, num_splits=num_splits)
+    torch.cuda.synchronize()
+    assert_close(host_f32(out), ref, f"decode Hq={Hq} Hkv={Hkv} ctx={ctx} splits={num_splits}")
+
+
+@pytest.mark.parametrize("Hq,Hkv,ctx,max_ctx,splits", [
+    (16, 8, 513, 1024, None),     # config 1 shape (0.6B)
+    (32, 8, 4096, 32768, None),   # config 2 (4B)
+    (32, 8, 4096, 32768, 1),
+    (32, 8, 4096, 32768, 7),
+    (32, 8, 4096, 32768, 200),    # more splits than tiles: empty splits
+    (64, 8, 8192, 32768, None),   # config 4 (32B)
+    (64, 8, 32768, 32768, None),
+    (8, 8, 1, 64, None),          # ctx = 1, G = 1
+    (32, 2, 100, 160, 3),         # ragged ctx, G = 16
+    (40, 8, 777, 1000, None),     # G = 5
+])
+def test_decode_attention_vs_oracle(gpu, Hq, Hkv, ctx, max_ctx, splits):
+    _decode_case(gpu, Hq, Hkv, ctx, max_ctx, splits, f"dec{Hq}_{ctx}")
+
+
+def test_decode_split_then_merge_matches_fused_call(gpu):
+    Hq, Hkv, ctx, max_ctx, ns = 32, 8, 3000, 4096, 11
+    q, kc, vc = normal("sq", (Hq, D)), normal("sk", (Hkv, max_ctx, D)), normal("sv", (Hkv, max_ctx, D))
+    p = torch.tensor([ctx - 1], dtype=torch.int32, device="cuda")
+    qd, kd, vd = dev(q), dev(kc), dev(vc)
+    acc, ml = gpu.ops.fmha_decode_gqa_split(qd, kd, vd, p, ns)
+    merged = gpu.ops.splitk_reduce_merge(acc, ml)
+    fused = gpu.ops.attn_decode(qd, kd, vd, p, num_splits=ns)
+    torch.cuda.synchronize()
+    assert torch.equal(merged, fused)
+    # partial statistics: sum over splits of l * 2^(m - M) equals the full softmax denominator
+    ml = ml.cpu().double()
+    M = ml[..., 0].max(1, keepdim=True).values
+    L = (ml[..., 1] * torch.exp2(ml[..., 0] - M)).sum(1)
+    qf = q.view(np.float16).astype(np.float64).reshape(Hkv, Hq // Hkv, D)
+    kf = kc[:, :ctx].view(np.float16).astype(np.float64)
+    s = np.einsum("hgd,hnd->hgn", qf, kf) / np.sqrt(D) * np.log2(np.e)
+    ref_L = np.exp2(s - M.numpy()[..., None][:, 0]).sum(-1)
+    assert np.allclose(L.numpy(), ref_L, rtol=2e-3)
+
+
+# ----------------------------------------------------------- prefill attention
+
+
+@pytest.mark.parametrize("S,Hq,Hkv,pos0", [
+    (1, 32, 8, 0), (17, 32, 8, 0), (64, 16, 8, 3), (200, 32, 8, 77), (130, 64, 8, 0),
+    (96, 8, 8, 10), (77, 40, 8, 9), (33, 16, 1, 0)])
+def test_prefill_attention_vs_oracle(gpu, S, Hq, Hkv, pos0):
+    _say("prefill", S, Hq, Hkv, pos0)
+    max_ctx = pos0 + S + 5
+    q = normal(f"pq{S}", (S, Hq, D))
+    kc, vc = normal(f"pk{S}", (Hkv, max_ctx, D)), normal(f"pv{S}", (Hkv, max_ctx, D))
+    ref = O.attention_prefill_rows(q, kc, vc, pos0, nthreads=8)
+    out = gpu.ops.fmha_prefill(dev(q), dev(kc), dev(vc), pos0)
+    torch.cuda.synchronize()
+    assert_close(host_f32(out), ref, f"prefill S={S} Hq={Hq} Hkv={Hkv} pos0={pos0}")
+
+
+# ------------------------------------------------------- configs end to end
+
+
+def test_config1_decode_step_pipeline(gpu):
+    """Qwen3-0.6B-shaped decode step: 512 cached positions, new token's q,k,v
+    through QK-RMSNorm + RoPE (pos 512, theta 1e6, eps 1e-6), KV write at slot
+    512, attention over 513 positions with scale 1/sqrt(128)."""
+    Hq, Hkv, pos, max_ctx = 16, 8, 512, 1024
+    kc = normal("c1k", (Hkv, max_ctx, D))
+    vc = normal("c1v", (Hkv, max_ctx, D))
+    kc[:, pos + 1:] = 0
+    vc[:, pos + 1:] = 0
+    qkv = normal("c1qkv", ((Hq + 2 * Hkv) * D,))
+    gq, gk = gamma("c1gq"), gamma("c1gk")
+    cos, sin = O.rope_table(max_ctx, D, 1e6)
+    kc_ref, vc_ref = kc.copy(), vc.copy()
+    q_ref = O.qk_norm_rope_kv_decode(qkv, gq, gk, cos, sin, kc_ref, vc_ref, pos, Hq, Hkv, 1e-6)
+    out_ref = O.attention_decode(q_ref, kc_ref, vc_ref, pos)
+
+    rope = gpu.ops.rope_tables(max_ctx)
+    kd, vd = dev(kc), dev(vc)
+    p = torch.tensor([pos], dtype=torch.int32, device="cuda")
+    q_rope = gpu.ops.qk_norm_rope_kv_decode(dev(qkv), dev(gq), dev(gk), rope, kd, vd, p, Hq)
+    out = gpu.ops.attention(q_rope.view(1, Hq, D), kd, vd, p)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(kd), kc_ref) and np.array_equal(host(vd), vc_ref)
+    assert_close(host_f32(out).reshape(Hq, D), out_ref, "config1 decode step")
+
+
+@pytest.mark.parametrize("S", [512, 2048])
+def test_config3_prefill_pipeline(gpu, S):
+    """Qwen3-4B-shaped prefill: fused QK-norm/RoPE/KV write at positions
+    0..S-1, then causal FMHA.  S=512 checked in full; S=2048 on rows 0..63,
+    the last 64 rows and 64 seeded random rows."""
+    _say("config3", S)
+    Hq, Hkv, max_ctx = 32, 8, 32768
+    q, k, v = normal(f"c3q{S}", (S, Hq, D)), normal(f"c3k{S}", (S, Hkv, D)), normal(f"c3v{S}", (S, Hkv, D))
+    gq, gk = gamma("c3gq"), gamma("c3gk")
+    cos, sin = O.rope_table(max_ctx, D, 1e6)
+    kc_ref = np.zeros((Hkv, max_ctx, D), np.uint16)
+    vc_ref = kc_ref.copy()
+    q_ref = O.qk_norm_rope_kv_prefill(q, k, v, gq, gk, cos, sin, kc_ref, vc_ref, 0, 1e-6)
+    rows = np.arange(S) if S <= 512 else np.unique(np.concatenate([
+        np.arange(64), np.arange(S - 64, S), np.random.default_rng(S).integers(0, S, 64)]))
+    ref = O.attention_prefill_rows(q_ref, kc_ref, vc_ref, 0, rows=rows, nthreads=16)
+
+    rope = gpu.ops.rope_tables(max_ctx)
+    kd = torch.zeros((Hkv, max_ctx, D), dtype=torch.float16, device="cuda")
+    vd = torch.zeros_like(kd)
+    q_rope = gpu.ops.qk_norm_rope_kv_prefill(dev(q), dev(k), dev(v), dev(gq), dev(gk), rope, kd, vd, 0)
+    out = gpu.ops.attention(q_rope, kd, vd, 0)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(q_rope), q_ref)
+    assert np.array_equal(host(kd[:, :S]), kc_ref[:, :S]) and np.array_equal(host(vd[:, :S]), vc_ref[:, :S])
+    assert_close(host_f32(out)[rows], ref, f"config3 prefill S={S}")
+
+
+def test_prefill_row_equals_decode_at_same_position(gpu):
+    """Prefill row m and a decode step at position m read the same cache: equal within tolerance."""
+    S, Hq, Hkv, max_ctx = 300, 32, 8, 512
+    q = normal("xq", (S, Hq, D))
+    kd, vd = dev(normal("xk", (Hkv, max_ctx, D))), dev(normal("xv", (Hkv, max_ctx, D)))
+    qd = dev(q)
+    pre = gpu.ops.fmha_prefill(qd, kd, vd, 0)
+    for m in (0, 31, 32, 255, 299):
+        p = torch.tensor([m], dtype=torch.int32, device="cuda")
+        dec = gpu.ops.attn_decode(qd[m], kd, vd, p)
+        torch.cuda.synchronize()
+        assert_close(host_f32(dec), host_f32(pre[m]), f"prefill row {m} vs decode")
+
+
+# ------------------------------------------------------------- decode graph
+
+
+def test_decode_graph_replays_match_eager_ops(gpu):
+    from grout_amd.engine import AttentionConfig, AttentionEngine
+
+    cfg = AttentionConfig(num_layers=3, num_attention_heads=32, num_key_value_heads=8, max_ctx=2048)
+    qn = [dev(gamma(f"gq{i}")) for i in range(3)]
+    kn = [dev(gamma(f"gk{i}")) for i in range(3)]
+    eng = AttentionEngine(cfg, qn, kn)
+    for i in range(3):  # prior context
+        eng.k_caches[i].copy_(dev(normal(f"gk_c{i}", (8, 2048, D))))
+        eng.v_caches[i].copy_(dev(normal(f"gv_c{i}", (8, 2048, D))))
+    graph = eng.build_decode_graph()
+    eager_k = [t.clone() for t in eng.k_caches]
+    eager_v = [t.clone() for t in eng.v_caches]
+    for step, pos in enumerate([700, 701, 1500, 2047]):
+        _say("graph replay", step, pos)
+        for i in range(3):
+            graph.qkv[i].copy_(dev(normal(f"gqkv{step}_{i}", ((32 + 16) * D,))))
+        graph.launch_step(pos)
+        torch.cuda.synchronize()
+        p = torch.tensor([pos], dtype=torch.int32, device="cuda")
+        for i in range(3):
+            qr = gpu.ops.qk_norm_rope_kv_decode(graph.qkv[i], qn[i], kn[i], eng.rope, eager_k[i],
+                                                eager_v[i], p, 32)
+            ref = gpu.ops.attn_decode(qr, eager_k[i], eager_v[i], p, num_splits=graph.num_splits)
+            torch.cuda.synchronize()
+            assert torch.equal(eng.k_caches[i], eager_k[i]) and torch.equal(eng.v_caches[i], eager_v[i])
+            assert torch.equal(graph.attn_out[i], ref), f"layer {i} step {step}"
+        torch.cuda.synchronize()
+    graph.destroy()
+    with pytest.raises(ValueError):
+        AttentionEngine(AttentionConfig(1, 32, 8, head_dim=64), qn[:1], kn[:1])
