@@ -76,6 +76,7 @@ int check_stride(long kv_head_stride, long min_rows) {
 constexpr int kMaxDecodeGroup = 16;
 constexpr int kMaxSplits = 4096;
 
+// Workspace layout: part_acc [Hkv][splits][G][128] f32 | part_ml [Hkv][splits][G][2] f32.
 size_t decode_ws_bytes(int hq, int hkv, int nsplit) {
   const size_t g = (size_t)(hq / hkv);
   return (size_t)hkv * nsplit * g * (128 + 2) * sizeof(float);
@@ -188,10 +189,11 @@ int grout_attn_decode_default_splits(int ctx_len, int num_q_heads, int num_kv_he
   if (ctx_len < 1 || num_kv_heads < 1) return 1;
   (void)num_q_heads;
   const int tiles = (ctx_len + 31) / 32;
-  // About 512 workgroups (two per CU) at long context; at least 8 tiles
-  // (2 per wave) per workgroup so short contexts do not scatter into empty splits.
-  int by_work = (tiles + 7) / 8;
-  int by_grid = (512 + num_kv_heads - 1) / num_kv_heads;
+  // One workgroup per CU over the 256 CUs at long context (measured best on
+  // MI355X for 4k..32k; more splits only add merge work), and at least 4
+  // tiles (one per wave) per workgroup at short context.
+  int by_work = (tiles + 3) / 4;
+  int by_grid = (256 + num_kv_heads - 1) / num_kv_heads;
   int n = by_work < by_grid ? by_work : by_grid;
   if (n < 1) n = 1;
   if (n > kMaxSplits) n = kMaxSplits;
@@ -248,19 +250,28 @@ int grout_attn_decode(const void* q, const void* k_cache, const void* v_cache, v
   GROUT_CHECK(check_heads(num_q_heads, num_kv_heads, head_dim, kMaxDecodeGroup));
   if (num_splits <= 0) num_splits = grout_attn_decode_default_splits(max_ctx, num_q_heads, num_kv_heads);
   GROUT_NEED(num_splits <= kMaxSplits, GROUT_EINVAL, "num_splits=%d > %d", num_splits, kMaxSplits);
+  GROUT_NEED(max_ctx >= 1, GROUT_EINVAL, "max_ctx=%d", max_ctx);
+  GROUT_NEED(std::isfinite(qk_scale) && qk_scale > 0.f, GROUT_EINVAL, "qk_scale=%g",
+             (double)qk_scale);
+  GROUT_NEED(d_pos != nullptr, GROUT_EINVAL, "d_pos is NULL");
   const size_t need = decode_ws_bytes(num_q_heads, num_kv_heads, num_splits);
   GROUT_NEED(workspace != nullptr && workspace_bytes >= need, GROUT_EINVAL,
              "workspace of %zu bytes < %zu needed for %d splits", workspace_bytes, need,
              num_splits);
-  GROUT_NEED(out != nullptr && aligned16(out), GROUT_EALIGN, "out is NULL or misaligned");
+  GROUT_CHECK(check_ptrs16({{q, "q"}, {k_cache, "k_cache"}, {v_cache, "v_cache"}, {out, "out"},
+                            {workspace, "workspace"}}));
+  GROUT_CHECK(check_stride(kv_head_stride, max_ctx));
   float* part_acc = static_cast<float*>(workspace);
   const size_t G = (size_t)(num_q_heads / num_kv_heads);
   float* part_ml = part_acc + (size_t)num_kv_heads * num_splits * G * 128;
-  GROUT_CHECK(grout_fmha_decode_gqa_split(q, k_cache, v_cache, part_acc, part_ml, d_pos,
-                                          num_q_heads, num_kv_heads, head_dim, max_ctx,
-                                          kv_head_stride, num_splits, qk_scale, stream));
-  return grout_splitk_reduce_merge(part_acc, part_ml, out, num_q_heads, num_kv_heads, head_dim,
-                                   num_splits, stream);
+  GROUT_CHECK(hip_status(grout::launch_attn_decode_split(q, k_cache, v_cache, kv_head_stride,
+                                                         d_pos, max_ctx, num_q_heads, num_kv_heads,
+                                                         num_splits, qk_scale, part_acc, part_ml,
+                                                         as_stream(stream)),
+                         "attn_decode split launch"));
+  return hip_status(grout::launch_attn_decode_merge(part_acc, part_ml, out, num_q_heads,
+                                                    num_kv_heads, num_splits, as_stream(stream)),
+                    "attn_decode merge launch");
 }
 
 // ------------------------------------------------------------------ graph

@@ -112,14 +112,16 @@ int grout_fmha_prefill(const void* q, const void* k_cache, const void* v_cache, 
 int grout_attn_decode_default_splits(int ctx_len, int num_q_heads, int num_kv_heads);
 
 /* Bytes of fp32 scratch grout_attn_decode needs for num_splits splits:
- * partial accumulators [Hkv][splits][G][128] + (max, sum) [Hkv][splits][G][2]. */
+ * partial accumulators [Hkv][splits][G][128] + (max, sum) [Hkv][splits][G][2].
+ * Calls sharing one workspace must not overlap in time. */
 size_t grout_attn_decode_workspace_bytes(int num_q_heads, int num_kv_heads, int head_dim,
                                          int num_splits);
 
 /* q [Hq][128] post-RoPE (q head h = kvh*G + g, i.e. the [Hkv][G][128] grouped
  * view), caches [Hkv][..][128], out [Hq][128].  Attends to positions
  * 0 .. d_pos[0] (s_kv = d_pos[0]+1, clamped to max_ctx).  num_splits <= 0
- * picks grout_attn_decode_default_splits(max_ctx, ...).
+ * picks grout_attn_decode_default_splits(max_ctx, ...).  Two launches
+ * (split pass, then the merge) on `stream`.
  * Replaces fmha_decode_gqa_split + splitk_reduce_merge
  * (src/kernels.rs:3996-4304) as recorded in src/model.rs:3713-3771. */
 int grout_attn_decode(const void* q, const void* k_cache, const void* v_cache, void* out,

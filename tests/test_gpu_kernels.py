@@ -128,6 +128,7 @@ def test_decode_split_then_merge_matches_fused_call(gpu):
     fused = gpu.ops.attn_decode(qd, kd, vd, p, num_splits=ns)
     torch.cuda.synchronize()
     assert torch.equal(merged, fused)
+    assert_close(host_f32(merged), O.attention_decode(q, kc, vc, ctx - 1, nthreads=8), "two-kernel path")
     # partial statistics: sum over splits of l * 2^(m - M) equals the full softmax denominator
     ml = ml.cpu().double()
     M = ml[..., 0].max(1, keepdim=True).values
@@ -137,6 +138,21 @@ def test_decode_split_then_merge_matches_fused_call(gpu):
     s = np.einsum("hgd,hnd->hgn", qf, kf) / np.sqrt(D) * np.log2(np.e)
     ref_L = np.exp2(s - M.numpy()[..., None][:, 0]).sum(-1)
     assert np.allclose(L.numpy(), ref_L, rtol=2e-3)
+
+
+def test_decode_reuses_workspace_across_calls(gpu):
+    """Consecutive decodes on one workspace (as the decode graph does)."""
+    Hq, Hkv, max_ctx, ns = 64, 8, 4096, 24
+    q, kc, vc = normal("wq", (Hq, D)), normal("wk", (Hkv, max_ctx, D)), normal("wv", (Hkv, max_ctx, D))
+    qd, kd, vd = dev(q), dev(kc), dev(vc)
+    ws = gpu.ops.decode_workspace(Hq, Hkv, ns, "cuda")
+    outs = []
+    for ctx in (4096, 1, 33, 2500, 4096, 700):
+        p = torch.tensor([ctx - 1], dtype=torch.int32, device="cuda")
+        outs.append((ctx, gpu.ops.attn_decode(qd, kd, vd, p, num_splits=ns, workspace=ws).clone()))
+    torch.cuda.synchronize()
+    for ctx, out in outs:
+        assert_close(host_f32(out), O.attention_decode(q, kc, vc, ctx - 1, nthreads=8), f"reuse ctx={ctx}")
 
 
 # ----------------------------------------------------------- prefill attention
