@@ -21,6 +21,10 @@ import sys
 import time
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+# HBM bytes per split-kernel launch (Qwen3-32B, ctx 32768, 32 splits) measured with
+# rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by a plain-copy calibration (x2.0, x1.0);
+# see profiles/attn_decode_split_qwen3-32b_ctx32768.md.
+DECODE32B_TRAFFIC_BYTES = 134.45e6 + 1.065e6
 F16_MFMA_PEAK_TFLOPS = 2516.6  # MI355X dense fp16 MFMA, TFLOP/s
 D = 128
 
@@ -32,10 +36,18 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--only", default="", help="comma list: decode32b,prefill,decode4b,norm")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch the timed calls from the host instead of replaying a captured "
+                         "graph (for per-dispatch counter collection)")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="also run a plain 256 MiB device copy (HBM counter calibration)")
     return ap.parse_args()
 
 
-def time_launches(fn, steps, warmup, stream=None, graph=True):
+GRAPH_TIMING = True
+
+
+def time_launches(fn, steps, warmup, stream=None, graph=None):
     """Average device time per call of fn(i) over `steps` back-to-back calls,
     bracketed by HIP events recorded on the stream the kernels are launched on.
     With graph=True the `steps` calls are first captured into one HIP graph
@@ -43,6 +55,7 @@ def time_launches(fn, steps, warmup, stream=None, graph=True):
     GPU idle between calls; the timed region is one replay of that graph."""
     import torch
 
+    graph = GRAPH_TIMING if graph is None else graph
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
@@ -213,7 +226,17 @@ def main():
     import grout_amd
     from grout_amd import ops
 
+    global GRAPH_TIMING
+    GRAPH_TIMING = not a.eager
     grout_amd.lib()
+    if a.copy_calib:
+        src = torch.ones(128 << 20, dtype=torch.float16, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"# copy_calib: 3 copies of {src.numel() * 2} bytes", file=sys.stderr, flush=True)
+        del src, dst
     only = set(filter(None, a.only.split(",")))
     want = lambda k: not only or k in only
     res = {}
@@ -245,7 +268,9 @@ def main():
                           "num_splits": r["num_splits"], "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
         line["roofline"] = {"bound": "hbm", "kernel": "attn_decode_split_kernel",
                             "achieved": round(split_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                            "frac": round(split_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                            "frac": round(split_gbs / HBM_PEAK_GBS, 4),
+                            "traffic": DECODE32B_TRAFFIC_BYTES if r["num_splits"] == 32 else None,
+                            "traffic_source": "profiles/attn_decode_split_qwen3-32b_ctx32768.md",
                             "kernel_us": round(r["split_ms"] * 1e3, 3),
                             "alg_bytes_per_launch": r["alg_bytes"]}
     if "prefill" in res:
