@@ -8,17 +8,23 @@
 // kv_head_stride, so the engine's [Hkv][max_ctx][D] cache works for every kv
 // head (the reference's LPT path assumes stride kv_len*D).
 //
-// gfx950 design (v_mfma_f32_16x16x32_f16, 256-thread workgroups):
+// gfx950 design (v_mfma_f32_16x16x32_f16, 256-thread workgroups, 2 per CU):
 //  * a workgroup owns up to 128 query rows = BQ query positions x HG heads of
 //    one kv group (HG = the largest divisor of G that is <= 8, BQ =
 //    floor(128/HG)), so every K/V tile staged in LDS serves HG heads; each
 //    wave owns 32 rows (two 16-column MFMA blocks);
+//  * K and V tiles (64 positions) are loaded with lane-contiguous 16-byte
+//    loads and stored row-major into double-buffered, XOR-swizzled LDS; the
+//    next tile is in flight while the current one is computed, with one
+//    workgroup barrier per tile;
 //  * S^T = K.Q^T (A = K rows from LDS, B = Q held in VGPRs for the whole
-//    loop) and O^T = V^T.P^T (A = V^T rows from LDS, B = P straight from the
-//    S^T accumulators): each query row is one lane column, so its softmax
-//    statistics never leave the lanes that own its accumulator;
-//  * K is staged row-major, V is staged transposed (d-major, with the
-//    position order of the P fragments), both with padded rows;
+//    loop) and O^T = V^T.P^T: the V^T fragments come straight from the
+//    row-major tile with ds_read_b64_tr_b16 (gfx950's transposing LDS read),
+//    P comes from the S^T accumulators without any shuffle, and each query
+//    row is one lane column, so its softmax statistics live in the lanes that
+//    own its accumulator;
+//  * the accumulator rescale is skipped when no row of the wave raised its
+//    running max (most tiles once the first few are in);
 //  * causal: tiles past the workgroup's last query are skipped, masks are
 //    applied only on tiles crossing the diagonal;
 //  * scheduling: block id -> (kv head = id mod Hkv, q block from the heavy
@@ -29,26 +35,37 @@
 
 namespace grout {
 
-constexpr int kBN = 64;                  // kv positions per tile
-constexpr int kKStride = kHeadDim + 8;   // halves per K row in LDS (272 B)
-constexpr int kVtStride = kBN + 8;       // halves per V^T row in LDS (144 B)
+constexpr int kBN = 64;                          // kv positions per tile
 constexpr int kRowsPerWG = 128;
+constexpr int kTileHalfBytes = kBN * kHeadDim * 2;  // 16 KiB: one of K or V
+constexpr int kStageBytes = 2 * kTileHalfBytes;     // K + V
 
-// Position (0..31) within a 32-position chunk -> its column in V^T, matching
-// the P fragment slot order: slot (kb, j) holds position 4kb+j (j<4) or
-// 16+4kb+(j-4) (j>=4).
-__device__ __forceinline__ int vt_perm(int p) {
-  return p < 16 ? 8 * (p >> 2) + (p & 3) : 8 * ((p - 16) >> 2) + 4 + (p & 3);
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v lds_short4;
+
+// Byte offset of 16-byte chunk `chunk` (0..15) of row `row` in a swizzled tile.
+__device__ __forceinline__ int pswz(int row, int chunk) {
+  return row * 256 + ((chunk ^ (row & 15)) << 4);
+}
+
+// ds_read_b64_tr_b16: inside each 16-lane group, lane i receives element
+// (i % 4) of the 8-byte chunks addressed by lanes i/4, i/4+4, i/4+8, i/4+12.
+// The result is bit-cast as a whole vector and two of them are joined with
+// one shuffle: extracting it element by element into a half8 was compiled
+// into a duplicate-low-half permute (only element 0 survived).
+__device__ __forceinline__ half4 lds_read_tr16(const unsigned char* p) {
+  const short4v v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_short4*)(__attribute__((address_space(3))) unsigned char*)(p));
+  return __builtin_bit_cast(half4, v);
 }
 
 template <int HG>
-__global__ __launch_bounds__(256) void fmha_prefill_kernel(
+__global__ __launch_bounds__(256, 2) void fmha_prefill_kernel(
     const half_t* __restrict__ q, const half_t* __restrict__ k_cache,
     const half_t* __restrict__ v_cache, half_t* __restrict__ out, int S, int pos0, int Hq,
     int Hkv, long head_stride, float scale_log2, int nqb) {
   constexpr int BQ = kRowsPerWG / HG;
-  __shared__ __attribute__((aligned(16))) half_t k_lds[kBN * kKStride];
-  __shared__ __attribute__((aligned(16))) half_t vt_lds[kHeadDim * kVtStride];
+  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * kStageBytes];  // 64 KiB
 
   const int G = Hq / Hkv;
   const int nsub = G / HG;
@@ -99,59 +116,46 @@ __global__ __launch_bounds__(256) void fmha_prefill_kernel(
 #pragma unroll
     for (int db = 0; db < 8; ++db) acc[mb][db] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  // Staging: thread -> K (chunk = tid%16, rows tid/16 + 16i) and V (chunk =
-  // tid%16, row pairs 2a,2a+1 in each 32-row half, a = tid/16).
-  const int chunk = tid & 15, rsel = tid >> 4;
+  // Staging: instruction i of thread tid covers row 16*i + tid/16, chunk tid%16
+  // (a wave instruction = 4 whole rows = 1 KiB, lane-contiguous).
+  const int srow = tid >> 4, schunk = tid & 15;
   u32x4 kreg[4], vreg[4];
   auto gload = [&](int tile) {
     const int kv0 = tile * kBN;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      int p = kv0 + rsel + 16 * i;
-      p = p < kv_len ? p : kv_len - 1;
-      kreg[i] = load16(kh + (size_t)p * kHeadDim + chunk * 8);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      int p = kv0 + 32 * (i >> 1) + 2 * rsel + (i & 1);
-      p = p < kv_len ? p : kv_len - 1;
-      vreg[i] = load16(vh + (size_t)p * kHeadDim + chunk * 8);
+      int p = kv0 + 16 * i + srow;
+      p = p < kv_len ? p : kv_len - 1;  // rows past kv_len are masked or unused
+      kreg[i] = load16(kh + (size_t)p * kHeadDim + schunk * 8);
+      vreg[i] = load16(vh + (size_t)p * kHeadDim + schunk * 8);
     }
   };
-  auto lds_store = [&]() {
+  auto lds_store = [&](unsigned char* st) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<u32x4*>(&k_lds[(rsel + 16 * i) * kKStride + chunk * 8]) = kreg[i];
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      const int colp = 32 * hh + vt_perm(2 * rsel);
-      const u32x4 a = vreg[2 * hh], b = vreg[2 * hh + 1];
-#pragma unroll
-      for (int wd = 0; wd < 4; ++wd) {
-        const uint32_t lo = (a[wd] & 0xffffu) | (b[wd] << 16);
-        const uint32_t hi = (a[wd] >> 16) | (b[wd] & 0xffff0000u);
-        const int d = chunk * 8 + 2 * wd;
-        *reinterpret_cast<uint32_t*>(&vt_lds[d * kVtStride + colp]) = lo;
-        *reinterpret_cast<uint32_t*>(&vt_lds[(d + 1) * kVtStride + colp]) = hi;
-      }
+    for (int i = 0; i < 4; ++i) {
+      const int row = 16 * i + srow;
+      *reinterpret_cast<u32x4*>(st + pswz(row, schunk)) = kreg[i];
+      *reinterpret_cast<u32x4*>(st + kTileHalfBytes + pswz(row, schunk)) = vreg[i];
     }
   };
 
   gload(0);
-  for (int tile = 0; tile < ntiles; ++tile) {
-    __syncthreads();
-    lds_store();
-    __syncthreads();
-    if (tile + 1 < ntiles) gload(tile + 1);
+  lds_store(smem);
+  if (ntiles > 1) gload(1);
+  __syncthreads();
 
+  for (int tile = 0; tile < ntiles; ++tile) {
+    const unsigned char* kst = smem + (tile & 1) * kStageBytes;
+    const unsigned char* vst = kst + kTileHalfBytes;
     const int kv0 = tile * kBN;
+
     floatx4 sc[2][4];
 #pragma unroll
     for (int pb = 0; pb < 4; ++pb) {
       half8 kf[4];
 #pragma unroll
       for (int c = 0; c < 4; ++c)
-        kf[c] = *reinterpret_cast<const half8*>(&k_lds[(16 * pb + col) * kKStride + c * 32 + kb * 8]);
+        kf[c] = as_half8(*reinterpret_cast<const u32x4*>(kst + pswz(16 * pb + col, 4 * c + kb)));
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
         floatx4 a = {0.f, 0.f, 0.f, 0.f};
@@ -163,6 +167,8 @@ __global__ __launch_bounds__(256) void fmha_prefill_kernel(
 
     const bool need_mask = kv0 + kBN - 1 > first_masked_kv;
     half8 pf[2][2];
+    bool grew = false;
+    float alpha[2];
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
       if (need_mask) {
@@ -182,7 +188,8 @@ __global__ __launch_bounds__(256) void fmha_prefill_kernel(
       tmax = fmaxf(tmax, shfl_xor(tmax, 16));
       tmax = fmaxf(tmax, shfl_xor(tmax, 32));
       const float mnew = fmaxf(m[mb], tmax * scale_log2);
-      const float alpha = fast_exp2(m[mb] - mnew);
+      grew |= mnew > m[mb];
+      alpha[mb] = fast_exp2(m[mb] - mnew);
       float psum = 0.f;
 #pragma unroll
       for (int pb = 0; pb < 4; ++pb)
@@ -192,21 +199,40 @@ __global__ __launch_bounds__(256) void fmha_prefill_kernel(
           psum += p;
           pf[mb][pb >> 1][(pb & 1) * 4 + i] = (half_t)p;
         }
-      l[mb] = l[mb] * alpha + psum;
+      l[mb] = l[mb] * alpha[mb] + psum;
       m[mb] = mnew;
+    }
+    if (__any(grew)) {  // wave-uniform: skip the rescale when no max moved
 #pragma unroll
-      for (int db = 0; db < 8; ++db) acc[mb][db] *= alpha;
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int db = 0; db < 8; ++db) acc[mb][db] *= alpha[mb];
     }
 
 #pragma unroll
     for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
       for (int db = 0; db < 8; ++db) {
-        const half8 vf = *reinterpret_cast<const half8*>(
-            &vt_lds[(16 * db + col) * kVtStride + 32 * cc + 8 * kb]);
+        // V^T fragment rows d = 16db + col, slots (kb, 0..7) = positions
+        // 32cc + {4kb..4kb+3, 16+4kb..16+4kb+3}: lane j of the 16-lane group
+        // addresses row 32cc + 16h + 4kb + j/4, d-chunk 16db + 4(j%4).
+        const int j = col;
+        const int cbyte = 32 * db + 8 * (j & 3);
+        const int r0 = 32 * cc + 4 * kb + (j >> 2);
+        const half4 lo = lds_read_tr16(vst + pswz(r0, cbyte >> 4) + (cbyte & 15));
+        const half4 hi = lds_read_tr16(vst + pswz(r0 + 16, cbyte >> 4) + (cbyte & 15));
+        const half8 vf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) acc[mb][db] = mfma16x16x32(vf, pf[mb][cc], acc[mb][db]);
       }
+
+    // Stage tile+1 into the other buffer (its last readers finished before the
+    // barrier that ended the previous iteration), then prefetch tile+2.
+    if (tile + 1 < ntiles) {
+      lds_store(smem + ((tile + 1) & 1) * kStageBytes);
+      if (tile + 2 < ntiles) gload(tile + 2);
+    }
+    __syncthreads();
   }
 
 #pragma unroll
