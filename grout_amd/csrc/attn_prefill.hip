@@ -47,13 +47,18 @@ namespace grout {
 constexpr int kBN = 64;  // kv positions per tile
 constexpr float kRescaleThreshold = 8.0f;
 constexpr int kRowsPerWG = 128;
-constexpr int kKRow = 272;                      // K row stride in LDS (256 B + 1 chunk)
-constexpr int kVRow = 288;                      // V row stride in LDS (256 B + 2 chunks)
-constexpr int kKBytes = kBN * kKRow;            // 17 KiB
-constexpr int kStageBytes = kKBytes + kBN * kVRow;  // 35 KiB: K + V of one tile
+constexpr int kRowBytes = kHeadDim * 2;        // 256 B: one K or V row
+constexpr int kTileBytes = kBN * kRowBytes;     // 16 KiB: one K or V tile
+
+// LDS swizzle of a 256-byte row: 16-byte chunk j of row r is stored at chunk
+// j ^ swz(r).  swz is a bijection on r % 16 (16 K rows reading one chunk hit 16
+// different chunks) and swz(r) >> 1 = r % 8 (8 consecutive V rows reading one
+// chunk pair hit 8 different pairs), so both fragment reads are conflict free.
+__device__ __forceinline__ int swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
 
 typedef short short4v __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4v lds_short4;
+typedef __attribute__((address_space(3))) void lds_void;
 
 // ds_read_b64_tr_b16: inside each 16-lane group, lane i receives element
 // (i % 4) of the 8-byte chunks addressed by lanes i/4, i/4+4, i/4+8, i/4+12.
@@ -66,19 +71,40 @@ __device__ __forceinline__ half4 lds_read_tr16(const unsigned char* p) {
   return __builtin_bit_cast(half4, v);
 }
 
+// Schedule of the P(t).V(t) + softmax(t+1) block: 36 MFMAs (32 P.V, 4 row
+// sums), 32 transposing LDS reads and about 80 VALU instructions (32 fma, 32
+// exp2, 16 packs).  Four reads go first; then each MFMA is followed by one
+// read and two VALU instructions, so one wave keeps both units busy.
+__device__ __forceinline__ void interleave_pv_softmax() {
+#ifndef GROUT_PREFILL_NO_INTERLEAVE
+  __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+  for (int i = 0; i < 28; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+  }
+#endif
+}
+
 template <int HG>
 __global__ __launch_bounds__(256, 2) void fmha_prefill_kernel(
     const half_t* __restrict__ q, const half_t* __restrict__ k_cache,
     const half_t* __restrict__ v_cache, half_t* __restrict__ out, int S, int pos0, int Hq,
     int Hkv, long head_stride, float scale_log2, int nqb) {
   constexpr int BQ = kRowsPerWG / HG;
-  // Two K slots and two V slots.  Iteration t reads K(t+1) and V(t); it
-  // stages K(t+2) into the K slot read in iteration t-1 and V(t+1) into the V
-  // slot read in iteration t-1, so one barrier per iteration suffices.
-  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * kStageBytes];
-  unsigned char* const kslot0 = smem;
-  unsigned char* const vslot0 = smem + 2 * kKBytes;
-  constexpr int kVBytes = kStageBytes - kKBytes;
+  // Two K slots and two V slots, each its own LDS object: the compiler then
+  // knows that the direct-to-LDS loads filling one slot do not alias the
+  // fragment reads of another and lets them stay in flight.
+  __shared__ __attribute__((aligned(1024))) unsigned char s_k0[kTileBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char s_k1[kTileBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char s_v0[kTileBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char s_v1[kTileBytes];
 
   const int G = Hq / Hkv;
   const int nsub = G / HG;
@@ -94,11 +120,12 @@ __global__ __launch_bounds__(256, 2) void fmha_prefill_kernel(
   const int q0 = qb * BQ;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, kb = lane >> 4;
 
-  const half_t* kh = k_cache + (size_t)kvh * head_stride;
-  const half_t* vh = v_cache + (size_t)kvh * head_stride;
+  const unsigned char* kh = reinterpret_cast<const unsigned char*>(k_cache + (size_t)kvh * head_stride);
+  const unsigned char* vh = reinterpret_cast<const unsigned char*>(v_cache + (size_t)kvh * head_stride);
   const int kv_len = pos0 + S;
 
   int qrow[2], qhead[2], qpos[2];
@@ -138,44 +165,62 @@ __global__ __launch_bounds__(256, 2) void fmha_prefill_kernel(
   const half8 ones = {(half_t)1.f, (half_t)1.f, (half_t)1.f, (half_t)1.f,
                       (half_t)1.f, (half_t)1.f, (half_t)1.f, (half_t)1.f};
 
-  // Staging: instruction i of thread tid covers row 16*i + tid/16, chunk
-  // tid%16 (a wave instruction = 4 whole rows = 1 KiB, lane-contiguous).
-  const int srow = tid >> 4, schunk = tid & 15;
-  auto gload_rows = [&](const half_t* base, int tile, u32x4 (&reg)[4]) {
-    const int kv0 = tile * kBN;
-    if (kv0 + kBN <= kv_len) {  // full tile: one base, constant offsets
-      const half_t* p = base + (size_t)(kv0 + srow) * kHeadDim + schunk * 8;
+  // Staging with global_load_lds: wave instruction i of wave w writes the
+  // 1 KiB of LDS holding tile rows 16w + 4i .. +3, lane l at byte 16*l, i.e.
+  // row 16w + 4i + l/16, stored chunk l%16, which holds logical chunk
+  // (l%16) ^ swz(row).  Each 16-lane group reads one whole 256-byte row.
+  int dma_row[4], dma_off[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) reg[i] = load16(p + 16 * i * kHeadDim);
+  for (int i = 0; i < 4; ++i) {
+    dma_row[i] = 16 * w + 4 * i + kb;
+    dma_off[i] = dma_row[i] * kRowBytes + ((col ^ swz(dma_row[i])) << 4);
+  }
+  auto dma_tile = [&](const unsigned char* base, int tile, unsigned char* slot) {
+    const int kv0 = tile * kBN;
+    if (kv0 + kBN <= kv_len) {
+      const unsigned char* p = base + (size_t)kv0 * kRowBytes;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        // Opaque to the optimizer, so the per-lane 64-bit sum is not hoisted
+        // out of the loop: a scalar base plus a 32-bit lane offset instead.
+        unsigned o = (unsigned)dma_off[i];
+        asm volatile("" : "+v"(o));
+        __builtin_amdgcn_global_load_lds(p + o, (lds_void*)(slot + (4 * w + i) * 1024), 16, 0, 0);
+      }
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        int pr = kv0 + 16 * i + srow;
-        pr = pr < kv_len ? pr : kv_len - 1;  // rows past kv_len are masked or unused
-        reg[i] = load16(base + (size_t)pr * kHeadDim + schunk * 8);
+        // rows past kv_len repeat the last row: masked for K, zero weight for V
+        unsigned o = (unsigned)dma_off[i];
+        asm volatile("" : "+v"(o));
+        const int pr = min(kv0 + dma_row[i], kv_len - 1);
+        const unsigned char* p = base + (size_t)pr * kRowBytes + (o & 255u);
+        __builtin_amdgcn_global_load_lds(p, (lds_void*)(slot + (4 * w + i) * 1024), 16, 0, 0);
       }
     }
   };
-  auto store_rows = [&](unsigned char* slot, int row_bytes, const u32x4 (&reg)[4]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<u32x4*>(slot + (16 * i + srow) * row_bytes + schunk * 16) = reg[i];
-  };
-  // Per-lane LDS bases of the fragment reads (all other terms are immediates):
-  //  K fragment (pb, c): row 16pb + col, 16-byte chunk 4c + kb;
+  // Per-lane LDS offsets of the fragment reads; row offsets are immediates.
+  //  K fragment (pb, c): row 16pb + col, logical chunk 4c + kb;
   //  V^T fragment (cc, db, half h): lane j of its 16-lane group addresses row
-  //  32cc + 16h + 4kb + j/4 at d = 16db + 4(j%4).
-  const int kfrag_base = col * kKRow + kb * 16;
-  const int vfrag_base = (4 * kb + (col >> 2)) * kVRow + 8 * (col & 3);
+  //  32cc + 16h + 4kb + j/4 at d = 16db + 4(j%4), i.e. logical chunk
+  //  2db + (j%4)/2, byte 8*(j%2) inside it.
+  int kfrag[4], vfrag[8];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) kfrag[c] = col * kRowBytes + (((4 * c + kb) ^ swz(col)) << 4);
+  {
+    const int vr = 4 * kb + (col >> 2), e = col & 3;
+#pragma unroll
+    for (int db = 0; db < 8; ++db)
+      vfrag[db] = vr * kRowBytes + (((2 * db + (e >> 1)) ^ swz(vr)) << 4) + ((e & 1) << 3);
+  }
 
   auto qk = [&](const unsigned char* kslot, floatx4 (&sc)[2][4]) {
-    const unsigned char* kst = kslot + kfrag_base;
 #pragma unroll
     for (int pb = 0; pb < 4; ++pb) {
       half8 kf[4];
 #pragma unroll
       for (int c = 0; c < 4; ++c)
-        kf[c] = as_half8(*reinterpret_cast<const u32x4*>(kst + 16 * pb * kKRow + 64 * c));
+        kf[c] = as_half8(*reinterpret_cast<const u32x4*>(kslot + kfrag[c] + 16 * pb * kRowBytes));
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
         floatx4 a = {0.f, 0.f, 0.f, 0.f};
@@ -224,15 +269,14 @@ __global__ __launch_bounds__(256, 2) void fmha_prefill_kernel(
               (half_t)fast_exp2(sc[mb][pb][i] * scale_log2 - m[mb]);
   };
   auto pv = [&](const unsigned char* vslot, const half8 (&pf)[2][2]) {
-    const unsigned char* vst = vslot + vfrag_base;
 #pragma unroll
     for (int cc = 0; cc < 2; ++cc) {
 #pragma unroll
       for (int db = 0; db < 8; ++db) {
         // V^T fragment rows d = 16db + col, slots (kb, 0..7) = positions
         // 32cc + {4kb..4kb+3, 16+4kb..16+4kb+3}.
-        const half4 lo = lds_read_tr16(vst + 32 * cc * kVRow + 32 * db);
-        const half4 hi = lds_read_tr16(vst + (32 * cc + 16) * kVRow + 32 * db);
+        const half4 lo = lds_read_tr16(vslot + vfrag[db] + 32 * cc * kRowBytes);
+        const half4 hi = lds_read_tr16(vslot + vfrag[db] + (32 * cc + 16) * kRowBytes);
         const half8 vf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) acc[mb][db] = mfma16x16x32(vf, pf[mb][cc], acc[mb][db]);
@@ -241,7 +285,9 @@ __global__ __launch_bounds__(256, 2) void fmha_prefill_kernel(
       for (int mb = 0; mb < 2; ++mb) lacc[mb] = mfma16x16x32(ones, pf[mb][cc], lacc[mb]);
     }
   };
-  auto rescale = [&](const float (&tmax)[2]) {
+  // Moves the running max to max(m, tmax); what was accumulated against the
+  // old max (acc, lacc and the not yet applied P(t)) is scaled by alpha.
+  auto rescale = [&](const float (&tmax)[2], half8 (&pf)[2][2]) {
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
       const float mnew = fmaxf(m[mb], tmax[mb]);
@@ -250,55 +296,59 @@ __global__ __launch_bounds__(256, 2) void fmha_prefill_kernel(
       lacc[mb] *= alpha;
 #pragma unroll
       for (int db = 0; db < 8; ++db) acc[mb][db] *= alpha;
+      const half_t ah = (half_t)alpha;
+      pf[mb][0] *= ah;
+      pf[mb][1] *= ah;
     }
   };
-
-  // ---- prologue: K0, V0 -> slot 0, K1 -> K slot 1; S(0) and P(0) ----
-  u32x4 kreg[4], vreg[4];
-  gload_rows(kh, 0, kreg);
-  gload_rows(vh, 0, vreg);
-  store_rows(kslot0, kKRow, kreg);
-  store_rows(vslot0, kVRow, vreg);
-  if (ntiles > 1) {
-    gload_rows(kh, 1, kreg);
-    store_rows(kslot0 + kKBytes, kKRow, kreg);
-  }
+  // ---- prologue: K0 -> s_k0, V0 -> s_v0, K1 -> s_k1; S(0) and P(0) ----
+  dma_tile(kh, 0, s_k0);
+  dma_tile(vh, 0, s_v0);
+  if (ntiles > 1) dma_tile(kh, 1, s_k1);
   __syncthreads();
 
   half8 pf[2][2];
   {
     floatx4 sc[2][4];
     float tmax[2];
-    qk(kslot0, sc);
-    if (tile_max(sc, 0, tmax)) rescale(tmax);
+    qk(s_k0, sc);
+    if (tile_max(sc, 0, tmax)) rescale(tmax, pf);  // acc and pf are still zero
     probs(sc, pf);
   }
-  __syncthreads();  // K slot 0 is restaged in iteration 0
+  __syncthreads();  // s_k0 is refilled in iteration 0
 
-  // Iteration t: phase A computes S(t+1) from K slot (t+1)&1 while V(t+1) is
-  // in flight to registers, then stages it into V slot (t+1)&1; phase B
-  // accumulates P(t).V(t) from V slot t&1 and turns S(t+1) into P(t+1) while
-  // K(t+2) is in flight, then stages it into K slot t&1.  Each staged slot
-  // was last read in iteration t-1, so one barrier per iteration suffices.
-  for (int t = 0; t < ntiles; ++t) {
+  // Iteration t reads K(t+1) and V(t) and, from its start, has V(t+1) and
+  // K(t+2) in flight into the two slots last read in iteration t-1; the
+  // barrier that ends the iteration waits for them.  S(t+1) comes first, so
+  // P(t).V(t) and the softmax of tile t+1 are independent work.
+  auto step = [&](int t, const unsigned char* kread, const unsigned char* vread,
+                  unsigned char* vfill, unsigned char* kfill) {
+    if (t + 1 < ntiles) dma_tile(vh, t + 1, vfill);
+    if (t + 2 < ntiles) dma_tile(kh, t + 2, kfill);
     if (t + 1 < ntiles) {
-      gload_rows(vh, t + 1, vreg);
       floatx4 sc[2][4];
       float tmax[2];
-      qk(kslot0 + ((t + 1) & 1) * kKBytes, sc);
-      const bool need = tile_max(sc, t + 1, tmax);
-      store_rows(vslot0 + ((t + 1) & 1) * kVBytes, kVRow, vreg);
-      if (t + 2 < ntiles) gload_rows(kh, t + 2, kreg);
-      // P(t).V(t) and the softmax of tile t+1 do not depend on each other:
-      // the exponentials overlap the MFMAs.
-      pv(vslot0 + (t & 1) * kVBytes, pf);
-      if (need) rescale(tmax);
-      probs(sc, pf);
-      if (t + 2 < ntiles) store_rows(kslot0 + (t & 1) * kKBytes, kKRow, kreg);
+      qk(kread, sc);
+      if (tile_max(sc, t + 1, tmax)) rescale(tmax, pf);
+      // P(t).V(t) and the softmax of tile t+1 are independent: one basic
+      // block whose schedule puts the exponentials under the MFMAs.
+      half8 pn[2][2];
+      pv(vread, pf);
+      probs(sc, pn);
+      interleave_pv_softmax();
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        pf[mb][0] = pn[mb][0];
+        pf[mb][1] = pn[mb][1];
+      }
     } else {
-      pv(vslot0 + (t & 1) * kVBytes, pf);
+      pv(vread, pf);
     }
     __syncthreads();
+  };
+  for (int t = 0; t < ntiles; t += 2) {
+    step(t, s_k1, s_v0, s_v1, s_k0);
+    if (t + 1 < ntiles) step(t + 1, s_k0, s_v1, s_v0, s_k1);
   }
 
 #pragma unroll
