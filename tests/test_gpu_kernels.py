@@ -172,6 +172,26 @@ def test_prefill_attention_vs_oracle(gpu, S, Hq, Hkv, pos0):
     assert_close(host_f32(out), ref, f"prefill S={S} Hq={Hq} Hkv={Hkv} pos0={pos0}")
 
 
+@pytest.mark.parametrize("teams", [1, 2])
+@pytest.mark.parametrize("S,Hq,Hkv,pos0", [
+    (1, 32, 8, 0), (17, 32, 8, 0), (130, 64, 8, 0), (200, 32, 8, 77), (77, 40, 8, 9),
+    (33, 16, 1, 0), (700, 32, 8, 100), (1000, 16, 4, 0)])
+def test_prefill_work_splits_vs_oracle(gpu, monkeypatch, teams, S, Hq, Hkv, pos0):
+    """Both work splits of the prefill kernel (one q block per 4-wave
+    workgroup; complementary q-block pairs split over two 4-wave teams with
+    an LDS merge), forced through GROUT_FMHA_PREFILL_TEAMS, on odd block
+    counts, a kv prefix (pos0 > 0) and a single kv head."""
+    monkeypatch.setenv("GROUT_FMHA_PREFILL_TEAMS", str(teams))
+    _say("prefill_split", teams, S, Hq, Hkv, pos0)
+    max_ctx = pos0 + S + 3
+    q = normal(f"wq{S}", (S, Hq, D))
+    kc, vc = normal(f"wk{S}", (Hkv, max_ctx, D)), normal(f"wv{S}", (Hkv, max_ctx, D))
+    ref = O.attention_prefill_rows(q, kc, vc, pos0, nthreads=16)
+    out = gpu.ops.fmha_prefill(dev(q), dev(kc), dev(vc), pos0)
+    torch.cuda.synchronize()
+    assert_close(host_f32(out), ref, f"prefill teams={teams} S={S} Hq={Hq} Hkv={Hkv} pos0={pos0}")
+
+
 # ------------------------------------------------------- configs end to end
 
 
