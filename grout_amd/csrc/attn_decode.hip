@@ -8,24 +8,26 @@
 // online softmax in exp2 units and the merge weights splits by 2^(m - max).
 //
 // gfx950 design (one workgroup = 4 waves per (split, kv head)):
-//  * a wave consumes 32-position tiles (tile index t = t0 + wave + 4i, so the
+//  * a wave consumes 16-position tiles (tile index t = t0 + wave + 4i, so the
 //    four waves of a workgroup stream adjacent tiles).  K and V rows are read
 //    with lane-contiguous 16-byte non-temporal loads (each wave instruction
-//    covers 1 KiB = 4 whole rows), the next tile is in flight while the
-//    current one is computed, and each wave re-lays its tile out through a
-//    private, XOR-swizzled LDS buffer into MFMA fragments (no workgroup
-//    barrier in the loop).  Reading rows directly in fragment order (16 rows
-//    x 64 B per instruction) measured ~15% below the lane-contiguous stream;
-//  * S^T = K.Q^T on v_mfma_f32_16x16x32_f16: A = 16 K rows (the natural
-//    row-major fragment), B = Q^T with the group's query heads as the 16
-//    columns (G <= 16, padded with zeros);
-//  * P.V needs V with positions along the reduction axis.  The row-major V
-//    fragment is turned around in registers by multiplying it with a 0/1
-//    selector on the MFMA unit (exact: every product is v*1 or v*0), which
-//    yields V^T fragments in the C layout, converted back to f16 losslessly;
-//  * O^T = V^T.P^T keeps each query head in one lane column, so the online
-//    softmax statistics (max, sum) of head g live in the lanes that own its
-//    accumulator: no cross-lane traffic for the rescale;
+//    covers 1 KiB = 4 whole rows, 8 KiB per tile), the next tile is in flight
+//    in registers while the current one is computed, and each wave re-lays
+//    its tile out through a private LDS buffer (no workgroup barrier in the
+//    loop), rows XOR-swizzled in 16-byte chunks so that both fragment reads
+//    below are bank-conflict free.  Small tiles measured faster than larger
+//    or deeper-buffered ones (32-position tiles, two tiles in flight, or a
+//    4-slot ring filled by direct-to-LDS loads): the memory system streams
+//    best with ~8 KiB per wave outstanding;
+//  * S^T = K.Q^T on v_mfma_f32_16x16x32_f16: A = the tile's 16 K rows, B = Q^T
+//    with the group's query heads as the 16 columns (G <= 16, zero padded);
+//  * O^T = V^T.P^T on v_mfma_f32_16x16x16_f16 (16 positions = its k): the
+//    V^T fragments come straight from the row-major tile with
+//    ds_read_b64_tr_b16 (gfx950's transposing LDS read), and P^T is the S^T
+//    accumulator layout as is, so each query head stays in one lane column
+//    and its online-softmax statistics live in the lanes that own its
+//    accumulator; the accumulator rescale is skipped unless some head's max
+//    grows by more than 2^8 (lazy rescale);
 //  * the 4 waves merge through LDS at the end and write one fp32 partial
 //    (unnormalized acc, max, sum) per (kv head, split, query head); a small
 //    second kernel merges the splits.  (Merging in the last workgroup of each
@@ -37,134 +39,37 @@
 
 namespace grout {
 
-constexpr int kTile = 32;  // kv positions per wave step
+constexpr int kTile = 16;    // kv positions per wave step
 constexpr int kDecWaves = 4;
+constexpr int kSlotBytes = 2 * kTile * kHeadDim * 2;  // 8 KiB per wave: K rows then V rows
+constexpr float kDecRescaleThreshold = 8.0f;
 
-// One tile (32 rows of K and of V) as loaded: instruction i of lane l holds
-// row 4i + l/16, 16-byte chunk l%16.
-struct KvRegs {
-  u32x4 k[8];
-  u32x4 v[8];
-};
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v lds_short4;
 
-__device__ __forceinline__ void load_kv_tile(KvRegs& r, const half_t* __restrict__ kh,
-                                             const half_t* __restrict__ vh, int tile, int s_kv,
-                                             int lane) {
-  const int sub = lane >> 4, chunk = lane & 15;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    int p = tile * kTile + 4 * i + sub;
-    p = p < s_kv ? p : s_kv - 1;  // rows past the context are masked; read a live row instead
-    r.k[i] = load_stream16(kh + (size_t)p * kHeadDim + chunk * 8);
-    r.v[i] = load_stream16(vh + (size_t)p * kHeadDim + chunk * 8);
-  }
+__device__ __forceinline__ floatx4 mfma16x16x16(half4 a, half4 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
 
-// Wave-private LDS tile: [K rows 0..31 | V rows 0..31], 256 B per row, the
-// 16-byte chunk c of row r stored at chunk slot c ^ (r & 15) so that both the
-// row-contiguous stores and the 16-rows-per-chunk fragment reads are
-// conflict-free.
-constexpr int kTileBytes = 2 * kTile * kHeadDim * 2;  // 16 KiB
-
-__device__ __forceinline__ int swz(int row, int chunk) { return row * 256 + ((chunk ^ (row & 15)) << 4); }
-
-__device__ __forceinline__ void store_kv_tile(unsigned char* buf, const KvRegs& r, int lane) {
-  const int sub = lane >> 4, chunk = lane & 15;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int row = 4 * i + sub;
-    *reinterpret_cast<u32x4*>(buf + swz(row, chunk)) = r.k[i];
-    *reinterpret_cast<u32x4*>(buf + kTile * 256 + swz(row, chunk)) = r.v[i];
-  }
-}
-
-// MFMA A fragment of 16 rows starting at row0 for d in [32c, 32c+32): lane l
-// gets row row0 + l%16, chunk 4c + l/16.
-__device__ __forceinline__ half8 frag(const unsigned char* base, int row0, int c, int lane) {
-  const int row = row0 + (lane & 15);
-  return as_half8(*reinterpret_cast<const u32x4*>(base + swz(row, 4 * c + (lane >> 4))));
-}
-
-struct DecState {
-  float m;  // running max (log2 units) of this lane's query head column
-  float l;  // this lane's partial sum of exp2 (reduced over the 4 lane groups at the end)
-  floatx4 acc[8];  // O^T fragments: d = 16*db + 4*(lane/16) + i, head = lane%16
-};
-
-__device__ __forceinline__ void compute_kv_tile(DecState& st, const unsigned char* buf,
-                                                const half8 (&qf)[4], const half8 (&sel)[2],
-                                                int tile, int s_kv, float scale_log2, int lane) {
-  const int kb = lane >> 4;
-  const unsigned char* vbuf = buf + kTile * 256;
-  floatx4 sc[2];
-#pragma unroll
-  for (int pb = 0; pb < 2; ++pb) {
-    floatx4 a = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int c = 0; c < 4; ++c) a = mfma16x16x32(frag(buf, 16 * pb, c, lane), qf[c], a);
-    sc[pb] = a;
-  }
-  float s[8];
-  float tmax = -1.0e30f;
-#pragma unroll
-  for (int pb = 0; pb < 2; ++pb) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int pos = tile * kTile + pb * 16 + kb * 4 + i;
-      float val = sc[pb][i] * scale_log2;
-      val = pos < s_kv ? val : -1.0e30f;
-      s[pb * 4 + i] = val;
-      tmax = fmaxf(tmax, val);
-    }
-  }
-  tmax = fmaxf(tmax, shfl_xor(tmax, 16));
-  tmax = fmaxf(tmax, shfl_xor(tmax, 32));
-  const float mnew = fmaxf(st.m, tmax);
-  const float alpha = fast_exp2(st.m - mnew);
-  half8 pf;
-  float psum = 0.f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float p = fast_exp2(s[e] - mnew);
-    psum += p;
-    pf[e] = (half_t)p;
-  }
-  st.l = st.l * alpha + psum;
-  st.m = mnew;
-#pragma unroll
-  for (int db = 0; db < 8; ++db) st.acc[db] *= alpha;
-
-  const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const floatx4 t0 = mfma16x16x32(frag(vbuf, 0, c, lane), sel[h], zero);
-      const floatx4 t1 = mfma16x16x32(frag(vbuf, 16, c, lane), sel[h], zero);
-      half8 vt;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        vt[i] = (half_t)t0[i];
-        vt[4 + i] = (half_t)t1[i];
-      }
-      st.acc[2 * c + h] = mfma16x16x32(vt, pf, st.acc[2 * c + h]);
-    }
-  }
-}
+// Swizzle of a 256-byte row: 16-byte chunk j of row r is stored at chunk
+// j ^ dswz(r); a bijection on r % 16 whose upper three bits are r % 8.
+__device__ __forceinline__ int dswz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
 
 __global__ __launch_bounds__(kDecWaves * 64, 2) void attn_decode_split_kernel(
     const half_t* __restrict__ q, const half_t* __restrict__ k_cache,
     const half_t* __restrict__ v_cache, long head_stride, const uint32_t* __restrict__ d_pos,
     int max_ctx, int G, int nsplit, float scale_log2, float* __restrict__ part_acc,
     float* __restrict__ part_ml) {
-  // Tile buffers during the loop; reused for the cross-wave merge afterwards.
-  __shared__ __attribute__((aligned(16))) unsigned char s_tiles[kDecWaves * kTileBytes];
+  // Wave w's tile buffer is s_buf[w]; after the loop the buffers are reused
+  // for the cross-wave merge.
+  __shared__ __attribute__((aligned(1024))) unsigned char s_buf[kDecWaves][kSlotBytes];
   __shared__ float s_ml[kDecWaves][16][2];
-  float(*s_acc)[16][kHeadDim] = reinterpret_cast<float(*)[16][kHeadDim]>(s_tiles);
 
   const int split = blockIdx.x, kvh = blockIdx.y;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15, kb = lane >> 4;
+  const int wave_off = w * kSlotBytes;  // folded into the per-lane offsets below
 
   const uint32_t pos = d_pos[0];
   const int s_kv = pos >= (uint32_t)max_ctx ? max_ctx : (int)pos + 1;  // always in [1, max_ctx]
@@ -172,9 +77,23 @@ __global__ __launch_bounds__(kDecWaves * 64, 2) void attn_decode_split_kernel(
   const int per = (ntiles + nsplit - 1) / nsplit;
   const int t0 = split * per;
   const int t1 = min(t0 + per, ntiles);
+  // this wave's tiles: t0 + w + 4k, k = 0 .. nmine-1
+  const int nmine = t0 + w < t1 ? (t1 - t0 - w + kDecWaves - 1) / kDecWaves : 0;
 
-  const half_t* kh = k_cache + (size_t)kvh * head_stride;
-  const half_t* vh = v_cache + (size_t)kvh * head_stride;
+  // Wave w takes the split's tiles j = w + 4k, visited from j = rot on
+  // (cyclically; rot is a multiple of 4, so the tile sets stay disjoint).
+  // Splits start 256 KiB apart at 32k; staggering where each one starts
+  // spreads the concurrent reads over more HBM channels (measured a few
+  // percent at 4k context, within noise at 32k).
+  const int len = t1 - t0;
+  const int rot = len > 0 && len % 4 == 0 ? ((split * 7 + kvh * 3) % (len / 4)) * 4 : 0;
+  auto tile_of = [&](int k) __attribute__((always_inline)) {
+    const int x = w + kDecWaves * k + rot;
+    return t0 + (x >= len ? x - len : x);
+  };
+
+  const unsigned char* kh = reinterpret_cast<const unsigned char*>(k_cache + (size_t)kvh * head_stride);
+  const unsigned char* vh = reinterpret_cast<const unsigned char*>(v_cache + (size_t)kvh * head_stride);
 
   half8 qf[4];
 #pragma unroll
@@ -185,43 +104,113 @@ __global__ __launch_bounds__(kDecWaves * 64, 2) void attn_decode_split_kernel(
       qf[c] = as_half8(u32x4{0u, 0u, 0u, 0u});
     }
   }
-  half8 sel[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) sel[h][i] = (half_t)((kb * 8 + i == h * 16 + col) ? 1.0f : 0.0f);
 
-  DecState st;
-  st.m = -1.0e30f;
-  st.l = 0.f;
+  // Tile as loaded: instruction i (0..3) of lane l holds row 4i + l/16,
+  // logical chunk l%16, of K (rk[i]) and of V (rv[i]); it is stored at chunk
+  // (l%16) ^ dswz(row) of the wave's LDS tile.
+  u32x4 rk[4], rv[4];
+  auto load_tile = [&](int k) __attribute__((always_inline)) {
+    const int t = tile_of(k);
 #pragma unroll
-  for (int db = 0; db < 8; ++db) st.acc[db] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-  unsigned char* buf = s_tiles + w * kTileBytes;
-  KvRegs regs;
-  int t = t0 + w;
-  if (t < t1) load_kv_tile(regs, kh, vh, t, s_kv, lane);
-  while (t < t1) {
-    store_kv_tile(buf, regs, lane);  // program order keeps this wave's LDS reads after the stores
-    const int tn = t + kDecWaves;
-    if (tn < t1) load_kv_tile(regs, kh, vh, tn, s_kv, lane);
-    compute_kv_tile(st, buf, qf, sel, t, s_kv, scale_log2, lane);
-    t = tn;
+    for (int i = 0; i < 4; ++i) {
+      // rows past the context are masked; read a live row instead
+      const int row = min(t * kTile + 4 * i + kb, s_kv - 1);
+      const unsigned off = (unsigned)row * 256u + (unsigned)col * 16u;
+      rk[i] = load_stream16(kh + off);
+      rv[i] = load_stream16(vh + off);
+    }
+  };
+  int st_off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) st_off[i] = wave_off + (4 * i + kb) * 256 + ((col ^ dswz(4 * i + kb)) << 4);
+  auto store_tile = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      *reinterpret_cast<u32x4*>(&s_buf[0][0] + st_off[i]) = rk[i];
+      *reinterpret_cast<u32x4*>(&s_buf[0][0] + st_off[i] + 4096) = rv[i];
+    }
+  };
+  // Fragment offsets (this wave's slot base included):
+  //  K (A of S^T): row col, logical chunk 4c + kb;
+  //  V^T (A of O^T, via ds_read_b64_tr_b16): lane j of group kb addresses
+  //  row 4kb + j/4 at d = 16db + 4(j%4), i.e. logical chunk 2db + (j%4)/2,
+  //  byte 8*(j%2) inside it; lane i then holds V[4kb + k][16db + i], k < 4.
+  int kfrag[4], vfrag[8];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) kfrag[c] = wave_off + col * 256 + (((4 * c + kb) ^ dswz(col)) << 4);
+  {
+    const int vr = 4 * kb + (col >> 2), e = col & 3;
+#pragma unroll
+    for (int db = 0; db < 8; ++db)
+      vfrag[db] = wave_off + 4096 + vr * 256 + (((2 * db + (e >> 1)) ^ dswz(vr)) << 4) +
+                  ((e & 1) << 3);
   }
-  __syncthreads();  // all waves are done with their tile buffers before s_acc reuses them
+
+  float m = -1.0e30f;  // running max (log2 units) of head `col`
+  float l = 0.f;       // this lane's part of its sum of p (4 positions per tile)
+  floatx4 acc[8];      // O^T: d = 16db + 4kb + i, head col
+#pragma unroll
+  for (int db = 0; db < 8; ++db) acc[db] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int k, const unsigned char* slot) __attribute__((always_inline)) {
+    const int t = tile_of(k);
+    floatx4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      sc = mfma16x16x32(as_half8(*reinterpret_cast<const u32x4*>(slot + kfrag[c])), qf[c], sc);
+    // positions t*16 + 4kb + i; the ones past the context are masked
+    const int lim = s_kv - t * kTile - 4 * kb;
+    float tmax = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sc[i] = i < lim ? sc[i] * scale_log2 : -__builtin_inff();
+      tmax = fmaxf(tmax, sc[i]);
+    }
+    tmax = fmaxf(tmax, shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, shfl_xor(tmax, 32));
+    if (__any(tmax > m + kDecRescaleThreshold)) {
+      const float mn = fmaxf(m, tmax);
+      const float alpha = fast_exp2(m - mn);
+      m = mn;
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < 8; ++db) acc[db] *= alpha;
+    }
+    half4 pf;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float p = fast_exp2(sc[i] - m);
+      l += p;
+      pf[i] = (half_t)p;
+    }
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      const short4v v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_short4*)(__attribute__((address_space(3))) unsigned char*)(slot + vfrag[db]));
+      acc[db] = mfma16x16x16(__builtin_bit_cast(half4, v), pf, acc[db]);
+    }
+  };
+
+  if (nmine > 0) load_tile(0);
+  for (int k = 0; k < nmine; ++k) {
+    store_tile();  // after this wave's reads of the previous tile (LDS is in order)
+    if (k + 1 < nmine) load_tile(k + 1);
+    compute(k, &s_buf[0][0]);
+  }
+  __syncthreads();  // all waves are done with their tile buffers before they are reused
 
   // Per-wave statistics of head `col`, then merge the 4 waves through LDS.
-  float l = st.l;
+  float(*s_acc)[16][kHeadDim] = reinterpret_cast<float(*)[16][kHeadDim]>(&s_buf[0][0]);
   l += shfl_xor(l, 16);
   l += shfl_xor(l, 32);
   if (kb == 0) {
-    s_ml[w][col][0] = st.m;
+    s_ml[w][col][0] = m;
     s_ml[w][col][1] = l;
   }
 #pragma unroll
   for (int db = 0; db < 8; ++db)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s_acc[w][col][db * 16 + kb * 4 + i] = st.acc[db][i];
+    for (int i = 0; i < 4; ++i) s_acc[w][col][db * 16 + kb * 4 + i] = acc[db][i];
   __syncthreads();
 
   const size_t base = ((size_t)kvh * nsplit + split) * G;
