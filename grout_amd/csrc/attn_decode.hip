@@ -12,7 +12,7 @@
 //    four waves of a workgroup stream adjacent tiles).  K and V rows are read
 //    with lane-contiguous 16-byte non-temporal loads (each wave instruction
 //    covers 1 KiB = 4 whole rows, 8 KiB per tile), the next tile is in flight
-//    in registers while the current one is computed, and each wave re-lays
+//    in registers while the current one is stored and computed, and each wave re-lays
 //    its tile out through a private LDS buffer (no workgroup barrier in the
 //    loop), rows XOR-swizzled in 16-byte chunks so that both fragment reads
 //    below are bank-conflict free.  Small tiles measured faster than larger
@@ -123,11 +123,11 @@ __global__ __launch_bounds__(kDecWaves * 64, 2) void attn_decode_split_kernel(
   int st_off[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) st_off[i] = wave_off + (4 * i + kb) * 256 + ((col ^ dswz(4 * i + kb)) << 4);
-  auto store_tile = [&]() __attribute__((always_inline)) {
+  auto store_tile = [&](const u32x4 (&tk)[4], const u32x4 (&tv)[4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<u32x4*>(&s_buf[0][0] + st_off[i]) = rk[i];
-      *reinterpret_cast<u32x4*>(&s_buf[0][0] + st_off[i] + 4096) = rv[i];
+      *reinterpret_cast<u32x4*>(&s_buf[0][0] + st_off[i]) = tk[i];
+      *reinterpret_cast<u32x4*>(&s_buf[0][0] + st_off[i] + 4096) = tv[i];
     }
   };
   // Fragment offsets (this wave's slot base included):
@@ -191,10 +191,18 @@ __global__ __launch_bounds__(kDecWaves * 64, 2) void attn_decode_split_kernel(
     }
   };
 
+  // The loads of tile k+1 are issued before tile k is stored (two register
+  // copies), so they overlap the store as well as the compute.
   if (nmine > 0) load_tile(0);
   for (int k = 0; k < nmine; ++k) {
-    store_tile();  // after this wave's reads of the previous tile (LDS is in order)
+    u32x4 ck[4], cv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ck[i] = rk[i];
+      cv[i] = rv[i];
+    }
     if (k + 1 < nmine) load_tile(k + 1);
+    store_tile(ck, cv);  // after this wave's reads of the previous tile (LDS is in order)
     compute(k, &s_buf[0][0]);
   }
   __syncthreads();  // all waves are done with their tile buffers before they are reused
