@@ -8,128 +8,125 @@
 // kv_head_stride, so the engine's [Hkv][max_ctx][D] cache works for every kv
 // head (the reference's LPT path assumes stride kv_len*D).
 //
-// gfx950 design (v_mfma_f32_16x16x32_f16, 256-thread workgroups, 2 per CU):
-//  * a workgroup owns up to 128 query rows = BQ query positions x HG heads of
-//    one kv group (HG = the largest divisor of G that is <= 8, BQ =
-//    floor(128/HG)), so every K/V tile staged in LDS serves HG heads; each
-//    wave owns 32 rows (two 16-column MFMA blocks);
-//  * K and V tiles (64 positions) are loaded with lane-contiguous 16-byte
-//    loads and stored row-major into double-buffered LDS with padded rows
-//    (K: 272 B, V: 288 B).  The padding makes both fragment reads
-//    bank-conflict free (16 K rows of one 16-byte chunk shift by one chunk per
-//    row; the transposing V reads touch 8 rows x 2 chunks that shift by two
-//    chunks per row) and keeps every per-tile LDS offset a compile-time
-//    immediate on a per-lane base.  The next tile is in flight while the
-//    current one is computed, with one workgroup barrier per tile;
-//  * S^T = K.Q^T (A = K rows from LDS, B = Q held in VGPRs for the whole
-//    loop) and O^T = V^T.P^T: the V^T fragments come straight from the
-//    row-major tile with ds_read_b64_tr_b16 (gfx950's transposing LDS read),
-//    P comes from the S^T accumulators without any shuffle, and each query
-//    row is one lane column, so its softmax statistics live in the lanes that
-//    own its accumulator;
-//  * lazy rescale: a row's running max only moves when the tile's max
-//    exceeds it by more than kRescaleThreshold (log2 units), so p stays
-//    <= 2^8 (exact in f16, harmless in the fp32 accumulators) and the
-//    accumulator rescale is skipped on almost every tile after the first;
-//  * the softmax row sums come from the MFMA unit (an all-ones A fragment
-//    against the P fragment), not from VALU adds and cross-lane reductions;
-//  * causal: tiles past the workgroup's last query are skipped, masks are
-//    applied only on tiles crossing the diagonal;
-//  * scheduling: block id -> (kv head = id mod Hkv, q block): the first half
-//    of the grid takes the heavy q blocks in decreasing order, the second half
-//    their complements, so co-resident workgroups balance each CU; with
+// gfx950 design (v_mfma_f32_16x16x32_f16, one 512-thread workgroup per CU):
+//  * a team of 4 waves owns a q block of 128 query rows = BQ query positions
+//    x HG heads of one kv group (HG = the largest divisor of G that is <= 8,
+//    BQ = floor(128/HG)), so every K/V tile staged in LDS serves HG heads;
+//    each wave owns 32 rows (two 16-column MFMA blocks);
+//  * the workgroup holds two teams, A = waves 0-3 and B = waves 4-7, one wave
+//    of each per SIMD.  Per kv tile a team runs two phases: G (the MFMA work:
+//    P(j).V(j) and S(j+1) = Q.K(j+1)^T) and S (the VALU work: mask, row max,
+//    exp2, P(j+1) and its row sums).  Team B runs one phase behind team A and
+//    every phase ends in a workgroup barrier, so on every SIMD one wave feeds
+//    the matrix core while the other runs the softmax ("ping-pong");
+//  * causal balance: workgroup r owns the complementary q blocks h = nqb-1-r
+//    and l = r (their tile counts add up to a constant).  Team A takes tiles
+//    [0, a) of h, team B all tiles of l and then tiles [a, T_h) of h, with
+//    a = ceil((T_h + T_l) / 2); B's partial (m, l, acc) of h is merged into
+//    A's through LDS at the end.  With too few pairs to fill the GPU each
+//    workgroup takes a single q block (T_l = 0), heaviest first;
+//  * K and V tiles (64 positions, 16 KiB each) go straight from the cache into
+//    double-buffered, XOR-swizzled LDS slots with buffer_load ... lds.  A
+//    per-tile buffer resource bounds the read at kv_len, so rows past the end
+//    arrive as zeros with no per-lane address arithmetic or clamping.  Loads
+//    for tiles j+2 (K) and j+1 (V) are issued in the S phase of tile j and
+//    have three phases to land: the barriers order LDS only and each wave
+//    waits for its own older loads (vmcnt) before the barrier that publishes
+//    them;
+//  * S^T = K.Q^T (A = K rows from LDS, B = Q held in VGPRs) and
+//    O^T = V^T.P^T (the V^T fragments come straight from the row-major tile
+//    with ds_read_b64_tr_b16, P from the S^T accumulators without a shuffle),
+//    so each query row is one lane column and its softmax statistics live in
+//    the lanes that own its accumulator; row reductions across the four lane
+//    groups use v_permlane16/32_swap, row sums v_dot2 on the f16 P values;
+//  * speculative softmax: P is computed against the running max as it
+//    stands and checked through its own row sums; only a tile whose scores
+//    rise ~8 (log2 units) above the running max (and the first tile of a
+//    block) pays for the exact row max, the rescale and a second pass, so
+//    p stays <= 2^8 (exact in f16) and most tiles cost 2 VALU ops per score
+//    plus the exp2;
+//  * scheduling: block id -> (kv head = id mod Hkv, q block pair), so with
 //    Hkv = 8 each XCD's L2 holds one kv head's K/V.
 #include "common.hpp"
 #include "kernels.hpp"
 
 #include <cstdlib>
+#include <type_traits>
 
 namespace grout {
 
 constexpr int kBN = 64;  // kv positions per tile
-constexpr float kRescaleThreshold = 8.0f;
-constexpr int kRowsPerWG = 128;
-constexpr int kRowBytes = kHeadDim * 2;        // 256 B: one K or V row
-constexpr int kTileBytes = kBN * kRowBytes;     // 16 KiB: one K or V tile
+// A lane's share of a tile row sum at or above this sends the tile down the
+// exact-max path of the speculative softmax (see s_phase).
+constexpr float kSpecLimit = 256.0f;
+constexpr int kRowsPerTeam = 128;
+constexpr int kRowBytes = kHeadDim * 2;     // 256 B: one K or V row
+constexpr int kTileBytes = kBN * kRowBytes;  // 16 KiB: one K or V tile
+// Buffer resource word 3 for raw (unswizzled, stride 0) 32-bit buffer access.
+constexpr int kBufferWord3 = 0x00020000;
 
-// LDS swizzle of a 256-byte row: 16-byte chunk j of row r is stored at chunk
-// j ^ swz(r).  swz is a bijection on r % 16 (16 K rows reading one chunk hit 16
-// different chunks) and swz(r) >> 1 = r % 8 (8 consecutive V rows reading one
-// chunk pair hit 8 different pairs), so both fragment reads are conflict free.
-__device__ __forceinline__ int swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+// LDS swizzles of a 256-byte row: 16-byte chunk j of row r is stored at
+// chunk j ^ swz(r).  K tiles use swz(r) = r % 16 (the 16 rows of a K fragment
+// read, one chunk each, spread over the banks at full ds_read_b128 rate; the
+// bijection ((r&7)<<1)|((r>>3)&1) measured at ~55% of it on gfx950).  V tiles
+// use swz_v(r) = ((r&7)<<1)|((r>>3)&1): swz_v(r) >> 1 = r % 8, so the 8
+// consecutive rows of a transposing read address 8 different chunk pairs.
+__device__ __forceinline__ int swz_v(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
 
 typedef short short4v __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4v lds_short4;
 typedef __attribute__((address_space(3))) void lds_void;
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 // ds_read_b64_tr_b16: inside each 16-lane group, lane i receives element
 // (i % 4) of the 8-byte chunks addressed by lanes i/4, i/4+4, i/4+8, i/4+12.
-// The result is bit-cast as a whole vector and two of them are joined with
-// one shuffle: extracting it element by element into a half8 was compiled
-// into a duplicate-low-half permute (only element 0 survived).
 __device__ __forceinline__ half4 lds_read_tr16(const unsigned char* p) {
   const short4v v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (lds_short4*)(__attribute__((address_space(3))) unsigned char*)(p));
   return __builtin_bit_cast(half4, v);
 }
 
-// Schedule of the P(t).V(t) + softmax(t+1) block: 36 MFMAs (32 P.V, 4 row
-// sums), 32 transposing LDS reads and about 80 VALU instructions (32 fma, 32
-// exp2, 16 packs).  Four reads go first; then each MFMA is followed by one
-// read and two VALU instructions, so one wave keeps both units busy.
-__device__ __forceinline__ void interleave_pv_softmax() {
-#ifndef GROUT_PREFILL_NO_INTERLEAVE
-  __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-  for (int i = 0; i < 28; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
-  }
-#endif
+// Workgroup barrier that orders LDS accesses only: this wave's LDS reads and
+// writes complete (lgkmcnt), direct-to-LDS loads in flight stay in flight.
+// A C++ release fence would also wait for every one of those loads (they
+// count as LDS writes), which would serialize the staging with the compute.
+// The "memory" clobber keeps the compiler from moving memory accesses across.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+// This wave's vector-memory operations except the 8 most recent (resp. all)
+// are complete.
+__device__ __forceinline__ void wait_vm_keep8() { asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); }
+__device__ __forceinline__ void wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Lane l ends with f(x[l], x[l ^ 16]) and then f(.., x[l ^ 32]): the reduction
+// over the four 16-lane groups that hold one MFMA column.
+__device__ __forceinline__ float col_max(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float col_sum(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// Schedule of the S(t+1) block: 16 K-fragment reads, 32 MFMAs and the 8
-// direct-to-LDS loads of the next tiles, one load after every two MFMAs.
-__device__ __forceinline__ void interleave_qk_dma() {
-  __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
-  }
-  __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
-}
-
-// One kernel, two work splits.
-//  TEAMS = 1: a 4-wave workgroup owns one q block (128 rows) and walks its
-//    causal kv tiles.
-//  TEAMS = 2: an 8-wave workgroup owns the complementary pair of q blocks
-//    h = nqb-1-r and l = r; team A (waves 0-3) takes tiles [0, a) of h, team
-//    B (waves 4-7) all tiles of l and then tiles [a, T_h) of h, with
-//    a = ceil((T_h + T_l) / 2), so the two teams do the same number of tiles
-//    and every workgroup the same work.  B's partial (m, l, acc) of h is merged
-//    into A's through LDS at the end.  The teams iterate in lockstep, one
-//    shared barrier per tile.
-template <int HG, int TEAMS>
-__global__ __launch_bounds__(256 * TEAMS, 2 / TEAMS) void fmha_prefill_kernel(
+template <int HG>
+__global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
     const half_t* __restrict__ q, const half_t* __restrict__ k_cache,
     const half_t* __restrict__ v_cache, half_t* __restrict__ out, int S, int pos0, int Hq,
-    int Hkv, long head_stride, float scale_log2, int nqb) {
-  constexpr int BQ = kRowsPerWG / HG;
+    int Hkv, long head_stride, float scale_log2, int nqb, int paired) {
+  constexpr int BQ = kRowsPerTeam / HG;
   // Per team: two K slots and two V slots, each slot its own LDS object, so
-  // the compiler knows that the direct-to-LDS loads filling one slot do not
-  // alias the fragment reads of another and lets them stay in flight.
-  __shared__ __attribute__((aligned(1024))) unsigned char s_k0[TEAMS][kTileBytes];
-  __shared__ __attribute__((aligned(1024))) unsigned char s_k1[TEAMS][kTileBytes];
-  __shared__ __attribute__((aligned(1024))) unsigned char s_v0[TEAMS][kTileBytes];
-  __shared__ __attribute__((aligned(1024))) unsigned char s_v1[TEAMS][kTileBytes];
+  // the compiler knows that the loads filling one slot do not alias the
+  // fragment reads of another and keeps them in flight.
+  __shared__ __attribute__((aligned(1024))) unsigned char s_k0[2][kTileBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char s_k1[2][kTileBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char s_v0[2][kTileBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char s_v1[2][kTileBytes];
 
   const int G = Hq / Hkv;
   const int nsub = G / HG;
@@ -142,52 +139,43 @@ __global__ __launch_bounds__(256 * TEAMS, 2 / TEAMS) void fmha_prefill_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int team = TEAMS == 2 ? wave >> 2 : 0;
+  const int team = wave >> 2;
   const int w = wave & 3;
   const int col = lane & 15, kb = lane >> 4;
+  const int kv_len = pos0 + S;
 
   auto tiles_of = [&](int qb) __attribute__((always_inline)) {
     const int q_last = min(qb * BQ + BQ, S) - 1;
     return (pos0 + q_last + 1 + kBN - 1) / kBN;
   };
-  // This team's kv tile sequence: n0 tiles of q block qb0 from tile tb0, then
-  // n1 tiles of q block qb1 from tile tb1.
-  int qb0, tb0 = 0, n0, qb1, tb1 = 0, n1 = 0, nloop, a_split = 0;
-  bool merge_h = false;    // team B holds part of block h (workgroup-uniform)
-  bool has_switch = false;  // team B moves from block l to block h (workgroup-uniform)
-  int switch_after = 0;     // ... after this many iterations (workgroup-uniform)
-  if (TEAMS == 1) {
-    // Blocks r and r + ceil(nqb/2) of a kv head take complementary q blocks;
-    // the heavy half is dispatched first.
-    const int half_q = (nqb + 1) / 2;
-    qb0 = r < half_q ? nqb - 1 - r : r - half_q;
-    qb1 = qb0;
-    n0 = tiles_of(qb0);
-    nloop = n0;
+  // Work split (workgroup-uniform): blocks h >= l, team A tiles [0, a) of h,
+  // team B tiles [0, tl) of l then [a, th) of h.
+  const int h = paired ? nqb - 1 - r : nqb - 1 - r;
+  const int l = paired ? r : h;
+  const int th = tiles_of(h), tl = h != l ? tiles_of(l) : 0;
+  const int a = (th + tl + 1) / 2;
+  const int nB = tl + th - a;
+  const bool merge_h = th > a;
+  // This team's tile sequence: n0 tiles of q block qb0 from tile tb0, then n1
+  // tiles of q block qb1 from tile tb1 (wave-uniform).
+  int qb0, tb0, n0, qb1, tb1, n1;
+  if (team == 0) {
+    qb0 = h; tb0 = 0; n0 = a; qb1 = h; tb1 = 0; n1 = 0;
+  } else if (tl > 0) {
+    qb0 = l; tb0 = 0; n0 = tl; qb1 = h; tb1 = a; n1 = th - a;
   } else {
-    const int h = nqb - 1 - r, l = r;
-    const int th = tiles_of(h), tl = h != l ? tiles_of(l) : 0;
-    a_split = (th + tl + 1) / 2;
-    merge_h = a_split < th;
-    has_switch = tl > 0 && merge_h;
-    switch_after = tl;
-    if (team == 0) {
-      qb0 = h; n0 = a_split; qb1 = h;
-    } else {
-      qb0 = l; n0 = tl; qb1 = h; tb1 = a_split; n1 = th - a_split;
-    }
-    nloop = a_split;  // team B has th + tl - a_split <= a_split tiles
+    qb0 = h; tb0 = a; n0 = th - a; qb1 = h; tb1 = 0; n1 = 0;
   }
   const int n = n0 + n1;
   auto tile_at = [&](int j) __attribute__((always_inline)) { return j < n0 ? tb0 + j : tb1 + (j - n0); };
+  auto qb_at = [&](int j) __attribute__((always_inline)) { return j < n0 ? qb0 : qb1; };
 
   const unsigned char* kh = reinterpret_cast<const unsigned char*>(k_cache + (size_t)kvh * head_stride);
   const unsigned char* vh = reinterpret_cast<const unsigned char*>(v_cache + (size_t)kvh * head_stride);
-  const int kv_len = pos0 + S;
 
   // Team t's slots sit t * kTileBytes above team 0's in every slot array;
-  // that offset is folded into the per-lane addresses below, so the slot
-  // arrays themselves stay compile-time constants (immediate offsets).
+  // the offset is folded into the per-lane addresses, so the slot arrays
+  // stay compile-time constants (immediate offsets).
   const int team_off = team * kTileBytes;
   unsigned char* const k0 = s_k0[0];
   unsigned char* const k1 = s_k1[0];
@@ -196,181 +184,273 @@ __global__ __launch_bounds__(256 * TEAMS, 2 / TEAMS) void fmha_prefill_kernel(
 
   // Row rr = 32w + 16mb + col of a q block is query position qb*BQ + rr/HG of
   // head kvh*G + hsub*HG + rr%HG.
-  auto row_pos = [&](int qb, int mb) __attribute__((always_inline)) { return qb * BQ + (32 * w + 16 * mb + col) / HG; };
-  auto row_head = [&](int mb) __attribute__((always_inline)) { return kvh * G + hsub * HG + (32 * w + 16 * mb + col) % HG; };
-  auto row_valid = [&](int qb, int mb) __attribute__((always_inline)) {
-    return 32 * w + 16 * mb + col < BQ * HG && row_pos(qb, mb) < S;
+  auto rpos = [&](int mb) __attribute__((always_inline)) { return (32 * w + 16 * mb + col) / HG; };
+  auto rhead = [&](int mb) __attribute__((always_inline)) {
+    return kvh * G + hsub * HG + (32 * w + 16 * mb + col) % HG;
   };
-  int qpos[2];
-  int first_masked_kv;  // a tile needs masking if it reaches past this
+  auto row_valid = [&](int qb, int mb) __attribute__((always_inline)) {
+    return 32 * w + 16 * mb + col < BQ * HG && qb * BQ + rpos(mb) < S;
+  };
+
   half8 qf[2][4];
   auto load_q = [&](int qb) __attribute__((always_inline)) {
-    first_masked_kv = pos0 + qb * BQ;
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
-      qpos[mb] = pos0 + row_pos(qb, mb);
       const bool valid = row_valid(qb, mb);
-      const half_t* qr = q + ((size_t)row_pos(qb, mb) * Hq + row_head(mb)) * kHeadDim + kb * 8;
+      const half_t* qr = q + ((size_t)(qb * BQ + rpos(mb)) * Hq + rhead(mb)) * kHeadDim + kb * 8;
 #pragma unroll
       for (int c = 0; c < 4; ++c)
         qf[mb][c] = valid ? as_half8(load16(qr + c * 32)) : as_half8(u32x4{0u, 0u, 0u, 0u});
     }
   };
 
-  // m: running max (log2 units) of row `col` of each block; lacc: its sum of
-  // p (every element of the C fragment holds it); acc: O^T fragments.  m
-  // starts finite and masked scores are -inf, so a row whose tiles so far are
-  // all masked keeps p = 0 (exp2(-inf)) instead of exp2(0).
-  float m[2];
-  floatx4 lacc[2], acc[2][8];
+  // m: running max (log2 units) of row `col`; lsum: this lane's share of its
+  // sum of p (the lane group kb covers 16 of every 64 positions); acc: O^T
+  // fragments.  m starts finite and masked scores are -inf, so a row whose
+  // tiles so far are all masked keeps p = 0 (exp2(-inf)) instead of exp2(0).
+  float m[2], lsum[2];
+  floatx4 acc[2][8];
+  auto reset_state = [&]() __attribute__((always_inline)) {
 #pragma unroll
-  for (int mb = 0; mb < 2; ++mb) {
-    m[mb] = -1.0e30f;
-    lacc[mb] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int mb = 0; mb < 2; ++mb) {
+      m[mb] = -1.0e30f;
+      lsum[mb] = 0.f;
 #pragma unroll
-    for (int db = 0; db < 8; ++db) acc[mb][db] = floatx4{0.f, 0.f, 0.f, 0.f};
-  }
-  const half8 ones = {(half_t)1.f, (half_t)1.f, (half_t)1.f, (half_t)1.f,
-                      (half_t)1.f, (half_t)1.f, (half_t)1.f, (half_t)1.f};
-
-  // Staging with global_load_lds: wave instruction i of wave w writes the
-  // 1 KiB of LDS holding tile rows 16w + 4i .. +3, lane l at byte 16*l, i.e.
-  // row 16w + 4i + l/16, stored chunk l%16, which holds logical chunk
-  // (l%16) ^ swz(row).  Each 16-lane group reads one whole 256-byte row.
-  // Row 16w + 4i + kb has swizzle swz(4i + kb).
-  const int dma_row0 = 16 * w + kb;
-  int dma_chunk[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) dma_chunk[i] = (col ^ swz(4 * i + kb)) << 4;
-  // Rows are clamped to kv_len - 1 (past the end they are masked for K and
-  // get zero weight for V); the code has no branch, so it can share a basic
-  // block, and hence an instruction schedule, with the MFMAs.
-  auto dma_tile = [&](const unsigned char* base, int tile, unsigned char* slot) __attribute__((always_inline)) {
-    const int kv0 = tile * kBN;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      // Opaque to the optimizer, so no per-lane 64-bit address is hoisted
-      // out of the loop: a scalar base plus a 32-bit lane offset instead.
-      unsigned o = (unsigned)dma_chunk[i];
-      asm volatile("" : "+v"(o));
-      const int pr = min(kv0 + dma_row0 + 4 * i, kv_len - 1);
-      const unsigned char* p = base + ((unsigned)pr * kRowBytes + o);  // < 2^32: rows*256 B
-      __builtin_amdgcn_global_load_lds(p, (lds_void*)(slot + team_off + (4 * w + i) * 1024),
-                                       16, 0, 0);
+      for (int db = 0; db < 8; ++db) acc[mb][db] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
   };
+  reset_state();
+
+  // Direct-to-LDS staging: wave instruction i of team wave w writes the 1 KiB
+  // of LDS holding tile rows 16w + 4i .. +3, lane l at byte 16*l, i.e. row
+  // 16w + 4i + l/16, stored chunk l%16, which holds logical chunk
+  // (l%16) ^ swz(row).  Each 16-lane group reads one whole 256-byte row.
+  // For these rows (r % 16 = 4i + kb) the K swizzle is 4i ^ kb and the V
+  // swizzle 2kb | 8(i&1) | (i>>1) (disjoint bits), so the source offset of
+  // instruction i is (dma0 ^ 16*c_i) + 1024i with c_i = 4i (K) or
+  // 8(i&1) | (i>>1) (V); the 1024i is the instruction's immediate offset,
+  // which moves the global and the LDS address alike.
+  const int dma0_k = (16 * w + kb) * kRowBytes + ((col ^ kb) << 4);
+  const int dma0_v = (16 * w + kb) * kRowBytes + ((col ^ (2 * kb)) << 4);
+  auto dma_tile = [&](auto is_v, const unsigned char* base, int tile, unsigned char* slot)
+                      __attribute__((always_inline)) {
+    constexpr bool V = decltype(is_v)::value;
+    const int valid_rows = kv_len - tile * kBN;  // >= 1 for every tile issued
+    __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<unsigned char*>(base) + (size_t)tile * kTileBytes, (short)0,
+        valid_rows * kRowBytes, kBufferWord3);
+    int o = V ? dma0_v : dma0_k;
+    asm volatile("" : "+v"(o));  // rebuilt per call, not held live across the loop
+    lds_void* const dst = (lds_void*)(slot + team_off + 4 * w * 1024);
+    constexpr int c1 = V ? 8 : 4, c2 = V ? 1 : 8, c3 = V ? 9 : 12;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 16, o, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 16, o ^ (c1 << 4), 0, 1024, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 16, o ^ (c2 << 4), 0, 2048, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 16, o ^ (c3 << 4), 0, 3072, 0);
+  };
+  const std::true_type is_v;
+  const std::false_type is_k;
+
   // Per-lane LDS offsets of the fragment reads; row offsets are immediates.
   //  K fragment (pb, c): row 16pb + col, logical chunk 4c + kb;
   //  V^T fragment (cc, db, half h): lane j of its 16-lane group addresses row
   //  32cc + 16h + 4kb + j/4 at d = 16db + 4(j%4), i.e. logical chunk
   //  2db + (j%4)/2, byte 8*(j%2) inside it.
-  int kfrag[4], vfrag[8];
-#pragma unroll
-  for (int c = 0; c < 4; ++c)
-    kfrag[c] = team_off + col * kRowBytes + (((4 * c + kb) ^ swz(col)) << 4);
+  // (4c + kb) ^ col = 4(c ^ (col>>2)) + (kb ^ (col&3)): the K offset of chunk
+  // group c is kfrag0 ^ 64c.  Likewise (2db + e/2) ^ swz_v(vr) =
+  // 2(db ^ (vr&7)) + (e/2 ^ (swz_v&1)): the V^T offset of block db is
+  // vfrag0 ^ 32db.  Bits 6-7 (K) and 5-7 (V) of the bases are free for the
+  // XOR constants.
+  int kfrag0, vfrag0;
   {
-    const int vr = 4 * kb + (col >> 2), e = col & 3;
-#pragma unroll
-    for (int db = 0; db < 8; ++db)
-      vfrag[db] = team_off + vr * kRowBytes + (((2 * db + (e >> 1)) ^ swz(vr)) << 4) +
-                  ((e & 1) << 3);
+    kfrag0 = team_off + col * kRowBytes + ((col >> 2) << 6) + ((kb ^ (col & 3)) << 4);
+    const int vr = 4 * kb + (col >> 2), e = col & 3, sv = swz_v(vr);
+    vfrag0 = team_off + vr * kRowBytes + ((vr & 7) << 5) + (((e >> 1) ^ (sv & 1)) << 4) +
+             ((e & 1) << 3);
   }
 
-  auto qk = [&](const unsigned char* kslot, floatx4 (&sc)[2][4]) __attribute__((always_inline)) {
+  floatx4 sc[2][4];   // S^T(j+1): element (pb, i) is kv position kv0 + 16pb + 4kb + i
+  half8 pf[2][2];     // P(j) as the B operand of P.V (positions 32cc + {4kb.., 16+4kb..})
+
+  // S(j+1) = K(j+1).Q^T (each K fragment serves both 16-row blocks).
+  auto qk = [&](const unsigned char* kread, int kbase) __attribute__((always_inline)) {
 #pragma unroll
     for (int pb = 0; pb < 4; ++pb) {
       half8 kf[4];
 #pragma unroll
       for (int c = 0; c < 4; ++c)
-        kf[c] = as_half8(*reinterpret_cast<const u32x4*>(kslot + kfrag[c] + 16 * pb * kRowBytes));
+        kf[c] = as_half8(*reinterpret_cast<const u32x4*>(kread + (kbase ^ (c << 6)) + 16 * pb * kRowBytes));
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
-        floatx4 a = {0.f, 0.f, 0.f, 0.f};
+        floatx4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int c = 0; c < 4; ++c) a = mfma16x16x32(kf[c], qf[mb][c], a);
-        sc[mb][pb] = a;
+        for (int c = 0; c < 4; ++c) s = mfma16x16x32(kf[c], qf[mb][c], s);
+        sc[mb][pb] = s;
       }
     }
   };
-  // Row maxima of a score tile (masked first when it crosses the diagonal).
-  // Returns whether any row of the wave must move its running max.
-  auto tile_max = [&](floatx4 (&sc)[2][4], int tile, float (&tmax)[2]) __attribute__((always_inline)) -> bool {
-    const int kv0 = tile * kBN;
-    bool need = false;
+  // G phase: P(j).V(j) into acc, then (unless j is the last tile) S(j+1), so
+  // P and the new scores are never live together.  The instruction order is
+  // fixed by hand (sched_barrier between groups):
+  //  * MFMAs that accumulate into the same registers run back to back (a
+  //    single wave feeding the matrix core runs at half rate when
+  //    consecutive MFMAs all read their accumulator from the register file,
+  //    and the scheduler would otherwise interleave independent chains);
+  //  * LDS under load answers in hundreds of cycles, so fragment reads run
+  //    four V blocks ahead, the K reads of pb 0-1 go under the last four V
+  //    blocks and those of pb 2-3 under the chains of pb 0-1.
+  auto g_phase = [&](auto with_qk, const unsigned char* kread, const unsigned char* vread)
+                     __attribute__((always_inline)) {
+    constexpr bool QK = decltype(with_qk)::value;
+    __builtin_amdgcn_s_setprio(1);
+    int vbase = vfrag0, kbase = kfrag0;
+    asm volatile("" : "+v"(vbase), "+v"(kbase));  // per-phase XORs, not 12 live registers
+    half8 vf[8][2];
+    half8 kf[4][4];
+    auto read_v = [&](int db) __attribute__((always_inline)) {
+      const int vo = vbase ^ (db << 5);
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      if (kv0 + kBN - 1 > first_masked_kv) {
+      for (int cc = 0; cc < 2; ++cc) {
+        const half4 lo = lds_read_tr16(vread + vo + 32 * cc * kRowBytes);
+        const half4 hi = lds_read_tr16(vread + vo + (32 * cc + 16) * kRowBytes);
+        vf[db][cc] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+    };
+    auto read_k = [&](int pb, int c) __attribute__((always_inline)) {
+      kf[pb][c] = as_half8(*reinterpret_cast<const u32x4*>(kread + (kbase ^ (c << 6)) + 16 * pb * kRowBytes));
+    };
+#pragma unroll
+    for (int db = 0; db < 4; ++db) read_v(db);
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        acc[mb][db] = mfma16x16x32(vf[db][0], pf[mb][0], acc[mb][db]);
+        acc[mb][db] = mfma16x16x32(vf[db][1], pf[mb][1], acc[mb][db]);
+      }
+      if (db + 4 < 8) {
+        read_v(db + 4);
+      } else if constexpr (QK) {
+        const int i = db - 4;  // K reads of pb 0-1: two per V block
+        read_k(i >> 1, 2 * (i & 1));
+        read_k(i >> 1, 2 * (i & 1) + 1);
+      }
+    }
+    if constexpr (QK) {
+#pragma unroll
+      for (int pb = 0; pb < 4; ++pb) {
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+          __builtin_amdgcn_sched_barrier(0);
+          floatx4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) a = mfma16x16x32(kf[pb][c], qf[mb][c], a);
+          sc[mb][pb] = a;
+          if (pb < 2) {
+            read_k(pb + 2, 2 * mb);
+            read_k(pb + 2, 2 * mb + 1);
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(0);
+  };
+  // QK only (the first tile of the team's sequence).
+  auto qk_only = [&](const unsigned char* kread) __attribute__((always_inline)) {
+    int kbase = kfrag0;
+    asm volatile("" : "+v"(kbase));
+    qk(kread, kbase);
+  };
+
+  // S phase of tile j: staging of K(j+2) and V(j+1) (repeats of the last tile
+  // past the end go to slots that are not read again, so every S phase issues
+  // exactly 8 loads per wave), the next segment's Q when tile j+1 starts one,
+  // then mask, row max, lazy rescale, P(j) and its row sums.  Ends with each
+  // wave's loads of the previous S phase complete.
+  auto s_phase = [&](int j, unsigned char* kfill, unsigned char* vfill) __attribute__((always_inline)) {
+    dma_tile(is_k, kh, tile_at(min(j + 2, n - 1)), kfill);
+    dma_tile(is_v, vh, tile_at(min(j + 1, n - 1)), vfill);
+    if (j + 1 == n0 && n1 > 0) {
+      // Once per workgroup: the next segment's Q, waited for here, so that
+      // no load into qf is pending where the paths join (the waitcnt pass
+      // would otherwise wait for every load in flight before each S.K^T).
+      load_q(qb1);
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    }
+    const int kv0 = tile_at(j) * kBN;
+    const int qrow0 = pos0 + qb_at(j) * BQ;  // first query position of the block
+    if (kv0 + kBN - 1 > qrow0) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
         // element (pb, i) is kv position kv0 + 4kb + 16pb + i: compare the
         // immediate 16pb + i against one per-lane limit
-        const int lim = qpos[mb] - kv0 - 4 * kb;
+        const int lim = qrow0 + rpos(mb) - kv0 - 4 * kb;
 #pragma unroll
         for (int pb = 0; pb < 4; ++pb)
 #pragma unroll
           for (int i = 0; i < 4; ++i)
             if (16 * pb + i > lim) sc[mb][pb][i] = -__builtin_inff();
       }
-      float t = -__builtin_inff();
-#pragma unroll
-      for (int pb = 0; pb < 4; ++pb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) t = fmaxf(t, sc[mb][pb][i]);
-      t = fmaxf(t, shfl_xor(t, 16));
-      t = fmaxf(t, shfl_xor(t, 32));
-      tmax[mb] = t * scale_log2;
-      need |= tmax[mb] > m[mb] + kRescaleThreshold;
     }
-    return __any(need);
-  };
-  auto probs = [&](const floatx4 (&sc)[2][4], half8 (&pf)[2][2]) __attribute__((always_inline)) {
+    // Speculative softmax: P against the running max m as it stands, and
+    // this lane's share of each row sum (16 scores).  A share of 2^8 or more
+    // (a score at least ~8 above m, an overflow to inf, or m still at its
+    // initial -1e30) sends the wave to the exact path: tile row max, rescale
+    // of what was accumulated, P again.  Accepted tiles keep p <= 2^8.
+    float ts[2];
+    auto probs = [&]() __attribute__((always_inline)) {
+      const half2v ones = {(half_t)1.f, (half_t)1.f};
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+      for (int mb = 0; mb < 2; ++mb) {
+        float s = 0.f;
 #pragma unroll
-      for (int pb = 0; pb < 4; ++pb)
+        for (int cc = 0; cc < 2; ++cc) {
+          half8 p;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          pf[mb][pb >> 1][(pb & 1) * 4 + i] =
-              (half_t)fast_exp2(sc[mb][pb][i] * scale_log2 - m[mb]);
-  };
-  auto pv = [&](const unsigned char* vslot, const half8 (&pf)[2][2]) __attribute__((always_inline)) {
+          for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-    for (int cc = 0; cc < 2; ++cc) {
-#pragma unroll
-      for (int db = 0; db < 8; ++db) {
-        // V^T fragment rows d = 16db + col, slots (kb, 0..7) = positions
-        // 32cc + {4kb..4kb+3, 16+4kb..16+4kb+3}.
-        const half4 lo = lds_read_tr16(vslot + vfrag[db] + 32 * cc * kRowBytes);
-        const half4 hi = lds_read_tr16(vslot + vfrag[db] + (32 * cc + 16) * kRowBytes);
-        const half8 vf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb) acc[mb][db] = mfma16x16x32(vf, pf[mb][cc], acc[mb][db]);
+            for (int i = 0; i < 4; ++i)
+              p[hh * 4 + i] = (half_t)fast_exp2(sc[mb][2 * cc + hh][i] * scale_log2 - m[mb]);
+          pf[mb][cc] = p;
+          s = __builtin_amdgcn_fdot2(__builtin_shufflevector(p, p, 0, 1), ones, s, false);
+          s = __builtin_amdgcn_fdot2(__builtin_shufflevector(p, p, 2, 3), ones, s, false);
+          s = __builtin_amdgcn_fdot2(__builtin_shufflevector(p, p, 4, 5), ones, s, false);
+          s = __builtin_amdgcn_fdot2(__builtin_shufflevector(p, p, 6, 7), ones, s, false);
+        }
+        ts[mb] = s;
       }
+    };
+    probs();
+    if (__any(ts[0] >= kSpecLimit || ts[1] >= kSpecLimit)) {
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) lacc[mb] = mfma16x16x32(ones, pf[mb][cc], lacc[mb]);
+      for (int mb = 0; mb < 2; ++mb) {
+        float t = fmaxf(sc[mb][0][0], sc[mb][0][1]);
+#pragma unroll
+        for (int pb = 0; pb < 4; ++pb)
+#pragma unroll
+          for (int i = (pb == 0 ? 2 : 0); i < 4; ++i) t = fmaxf(t, sc[mb][pb][i]);
+        const float mnew = fmaxf(m[mb], col_max(t) * scale_log2);
+        const float alpha = fast_exp2(m[mb] - mnew);
+        m[mb] = mnew;
+        lsum[mb] *= alpha;
+#pragma unroll
+        for (int db = 0; db < 8; ++db) acc[mb][db] *= alpha;
+      }
+      probs();
     }
+    lsum[0] += ts[0];
+    lsum[1] += ts[1];
+    wait_vm_keep8();
   };
-  // Moves the running max to max(m, tmax) for rows that saw a finite score;
-  // what was accumulated against the old max (acc, lacc and the not yet
-  // applied P(t)) is scaled by alpha.
-  auto rescale = [&](const float (&tmax)[2], half8 (&pf)[2][2]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      const float mnew = fmaxf(m[mb], tmax[mb]);
-      const float alpha = fast_exp2(m[mb] - mnew);
-      m[mb] = mnew;
-      lacc[mb] *= alpha;
-#pragma unroll
-      for (int db = 0; db < 8; ++db) acc[mb][db] *= alpha;
-      const half_t ah = (half_t)alpha;
-      pf[mb][0] *= ah;
-      pf[mb][1] *= ah;
-    }
-  };
-  auto write_out = [&](int qb) __attribute__((always_inline)) {
+
+  auto write_rows = [&](int qb, const float (&lrow)[2]) __attribute__((always_inline)) {
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
       if (!row_valid(qb, mb)) continue;
-      const float inv = 1.0f / lacc[mb][0];
-      half_t* orow = out + ((size_t)row_pos(qb, mb) * Hq + row_head(mb)) * kHeadDim;
+      const float inv = 1.0f / lrow[mb];
+      half_t* orow = out + ((size_t)(qb * BQ + rpos(mb)) * Hq + rhead(mb)) * kHeadDim;
 #pragma unroll
       for (int db = 0; db < 8; ++db) {
         half4 o;
@@ -380,119 +460,78 @@ __global__ __launch_bounds__(256 * TEAMS, 2 / TEAMS) void fmha_prefill_kernel(
       }
     }
   };
-
-  // ---- prologue: K(0) -> k0, V(0) -> v0, K(1) -> k1; S(0) and P(0) ----
-  // (for team B with a block-l segment, its first segment only)
-  // Both teams must run the same barriers, so the switch point is a property
-  // of the workgroup, not of the team.
-  const int n_first = team == 1 && has_switch ? switch_after : n;  // tiles before the switch
-  half8 pf[2][2];
-  if (n > 0) {
-    dma_tile(kh, tile_at(0), k0);
-    dma_tile(vh, tile_at(0), v0);
-    if (n_first > 1) dma_tile(kh, tile_at(1), k1);
-    load_q(n0 > 0 ? qb0 : qb1);
-  }
-  __syncthreads();
-  if (n > 0) {
-    floatx4 sc[2][4];
-    float tmax[2];
-    qk(k0, sc);
-    if (tile_max(sc, tile_at(0), tmax)) rescale(tmax, pf);  // acc is zero, pf not yet set
-    probs(sc, pf);
-  }
-  __syncthreads();  // k0 is refilled in iteration 0
-
-  // Iteration j reads K(j+1) and V(j) and, from its start, has V(j+1) and
-  // K(j+2) in flight into the two slots last read in iteration j-1; the
-  // barrier that ends the iteration waits for them.  S(j+1) comes first, so
-  // P(j).V(j) and the softmax of tile j+1 are independent work.  nn is the
-  // length of the team's current tile run.
-  auto step = [&](int j, int nn, const unsigned char* kread, const unsigned char* vread,
-                  unsigned char* vfill, unsigned char* kfill) __attribute__((always_inline)) {
-    if (j + 1 < nn) {
-      floatx4 sc[2][4];
-      float tmax[2];
-      // The eight loads spread over the S MFMAs instead of queueing behind
-      // one another at the top of the iteration.  Past the last tile the K
-      // load repeats it into a slot that is not read again.
-      dma_tile(kh, tile_at(min(j + 2, nn - 1)), kfill);
-      dma_tile(vh, tile_at(j + 1), vfill);
-      qk(kread, sc);
-      interleave_qk_dma();
-      if (tile_max(sc, tile_at(j + 1), tmax)) rescale(tmax, pf);
-      // P(j).V(j) and the softmax of tile j+1 are independent: one basic
-      // block whose schedule puts the exponentials under the MFMAs.
-      half8 pn[2][2];
-      pv(vread, pf);
-      probs(sc, pn);
-      interleave_pv_softmax();
+  auto row_sums = [&](float (&lrow)[2]) __attribute__((always_inline)) {
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
-        pf[mb][0] = pn[mb][0];
-        pf[mb][1] = pn[mb][1];
-      }
-    } else if (j + 1 == nn) {
-      pv(vread, pf);
-    }
-    __syncthreads();
+    for (int mb = 0; mb < 2; ++mb) lrow[mb] = col_sum(lsum[mb]);
   };
-  // Team B's move from block l to the tail of block h, run between
-  // iterations js = switch_after - 1 and js + 1 (both teams take part in its
-  // two barriers).  After iteration js the slots K (js+1)&1, K js&1 and
-  // V (js+1)&1 are free; iteration js+1 reads K(js+2) from K slot js&1 and
-  // V(js+1) from V slot (js+1)&1, and refills K slot (js+1)&1.
-  auto team_switch = [&](int js, unsigned char* kcur, unsigned char* knext,
-                         unsigned char* vcur) __attribute__((always_inline)) {
-    if (team == 1) {
-      write_out(qb0);
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
-        m[mb] = -1.0e30f;
-        lacc[mb] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int db = 0; db < 8; ++db) acc[mb][db] = floatx4{0.f, 0.f, 0.f, 0.f};
-      }
-      dma_tile(kh, tile_at(js + 1), kcur);
-      dma_tile(vh, tile_at(js + 1), vcur);
-      if (n1 > 1) dma_tile(kh, tile_at(js + 2), knext);
-      load_q(qb1);
+
+  // G phase of tile j plus, after the last tile of the first segment when a
+  // second one follows, that block's output and a fresh state.
+  auto g_step = [&](int j, const unsigned char* kread, const unsigned char* vread) __attribute__((always_inline)) {
+    if (j + 1 < n)
+      g_phase(std::true_type{}, kread, vread);
+    else
+      g_phase(std::false_type{}, kread, vread);
+    if (j + 1 == n0 && n1 > 0) {
+      float lrow[2];
+      row_sums(lrow);
+      write_rows(qb0, lrow);
+      reset_state();
     }
-    __syncthreads();
-    if (team == 1) {
-      floatx4 sc[2][4];
-      float tmax[2];
-      qk(kcur, sc);
-      if (tile_max(sc, tile_at(js + 1), tmax)) rescale(tmax, pf);
-      probs(sc, pf);
-    }
-    __syncthreads();  // K slot (js+1)&1 is refilled in iteration js+1
   };
-  // Slots by parity: even j reads K slot 1 / V slot 0, odd j the others;
-  // two sequential calls per trip (an if/else would be merged into one copy
-  // with runtime slot pointers).  Team B's run before the switch is
-  // switch_after tiles long.
-  const int js = has_switch ? switch_after - 1 : -2;
-  for (int j = 0; j < nloop; j += 2) {
-    if (j == js + 1) team_switch(js, k0, k1, v0);  // js odd: (js+1)&1 = 0
-    step(j, team == 1 && j <= js ? n_first : n, k1, v0, v1, k0);
-    if (j + 1 < nloop) {
-      if (j + 1 == js + 1) team_switch(js, k1, k0, v1);  // js even
-      step(j + 1, team == 1 && j + 1 <= js ? n_first : n, k0, v1, v0, k1);
+
+  // ---- prologue: K(0) -> k0, V(0) -> v0, K(1) -> k1, Q of the first block ----
+  if (n > 0) {
+    dma_tile(is_k, kh, tile_at(0), k0);
+    dma_tile(is_v, vh, tile_at(0), v0);
+    dma_tile(is_k, kh, tile_at(min(1, n - 1)), k1);
+    load_q(qb0);
+  }
+  wait_vm_all();
+  lds_barrier();
+  // Phase count after this point: A runs 1 + 2*nA phases, B one idle phase
+  // plus 1 + 2*nB; the shorter team pads with empty phases.
+  const int total = max(1 + 2 * a, 2 + 2 * nB);
+  int mine = 0;
+  if (team == 1) {
+    lds_barrier();
+    mine = 1;
+  }
+  if (n > 0) qk_only(k0);
+  lds_barrier();
+  mine += 1 + 2 * n;
+  // Tile j reads K slot (j+1)&1 and V slot j&1 in its G phase and refills K
+  // slot j&1 and V slot (j+1)&1 in its S phase.  Two tiles per trip, so the
+  // slot of every access is a compile-time constant.
+  for (int j = 0; j < n; j += 2) {
+    s_phase(j, k0, v1);
+    lds_barrier();
+    g_step(j, k1, v0);
+    lds_barrier();
+    if (j + 1 < n) {
+      s_phase(j + 1, k1, v0);
+      lds_barrier();
+      g_step(j + 1, k0, v1);
+      lds_barrier();
     }
   }
+  for (; mine < total; ++mine) lds_barrier();
+  // The last S phases' loads may still be landing in slots that the merge
+  // below reuses: every wave drains its own before one more barrier.
+  wait_vm_all();
+  lds_barrier();
 
-  if (TEAMS == 1 || !merge_h) {
-    // every team finished whole q blocks
-    if (n > 0) write_out(n1 > 0 ? qb1 : qb0);
+  float lrow[2];
+  row_sums(lrow);
+  if (!merge_h) {
+    if (n > 0) write_rows(n1 > 0 ? qb1 : qb0, lrow);
     return;
   }
   // Team B holds tiles [a, T_h) of block h: its (m, l, acc) go through LDS
-  // (its own K/V slots take acc, team A's first K slot takes m and l) and
-  // team A combines them with its own tiles [0, a).  Same wave index, same
-  // lane: same rows and columns.
-  unsigned char* const accbuf = w == 0 ? s_k0[TEAMS - 1] : w == 1 ? s_k1[TEAMS - 1]
-                              : w == 2 ? s_v0[TEAMS - 1] : s_v1[TEAMS - 1];
+  // (team 1's slots take acc, team 0's first K slot takes m and l) and team A
+  // combines them with its own tiles [0, a).  Same wave index, same lane:
+  // same rows and columns.
+  unsigned char* const accbuf = w == 0 ? s_k0[1] : w == 1 ? s_k1[1] : w == 2 ? s_v0[1] : s_v1[1];
   float* const mlbuf = reinterpret_cast<float*>(s_k0[0] + w * 1024) + lane * 4;
   if (team == 1) {
 #pragma unroll
@@ -500,28 +539,30 @@ __global__ __launch_bounds__(256 * TEAMS, 2 / TEAMS) void fmha_prefill_kernel(
 #pragma unroll
       for (int db = 0; db < 8; ++db)
         *reinterpret_cast<floatx4*>(accbuf + ((mb * 8 + db) * 64 + lane) * 16) = acc[mb][db];
-    *reinterpret_cast<floatx4*>(mlbuf) = floatx4{m[0], m[1], lacc[0][0], lacc[1][0]};
+    *reinterpret_cast<floatx4*>(mlbuf) = floatx4{m[0], m[1], lrow[0], lrow[1]};
   }
-  __syncthreads();
+  lds_barrier();
   if (team == 0) {
     const floatx4 mlb = *reinterpret_cast<const floatx4*>(mlbuf);
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
       const float mn = fmaxf(m[mb], mlb[mb]);
       const float sa = fast_exp2(m[mb] - mn), sb = fast_exp2(mlb[mb] - mn);
-      lacc[mb] = lacc[mb] * sa + mlb[2 + mb] * sb;
+      lrow[mb] = lrow[mb] * sa + mlb[2 + mb] * sb;
 #pragma unroll
       for (int db = 0; db < 8; ++db)
         acc[mb][db] = acc[mb][db] * sa +
                       *reinterpret_cast<const floatx4*>(accbuf + ((mb * 8 + db) * 64 + lane) * 16) * sb;
     }
-    write_out(qb0);
+    write_rows(h, lrow);
   }
 }
 
-static int prefill_teams_override() {
-  const char* e = std::getenv("GROUT_FMHA_PREFILL_TEAMS");
-  return e ? std::atoi(e) : 0;
+// GROUT_FMHA_PREFILL_PAIRED=0/1 forces the single-block / paired work split
+// (tests exercise both); by default pairs are used when they fill the GPU.
+static int prefill_paired_override() {
+  const char* e = std::getenv("GROUT_FMHA_PREFILL_PAIRED");
+  return e ? std::atoi(e) : -1;
 }
 
 hipError_t launch_fmha_prefill(const void* q, const void* k_cache, const void* v_cache,
@@ -531,26 +572,21 @@ hipError_t launch_fmha_prefill(const void* q, const void* k_cache, const void* v
   const int G = Hq / Hkv;
   int HG = 8;
   while (G % HG != 0) --HG;
-  const int BQ = kRowsPerWG / HG;
+  const int BQ = kRowsPerTeam / HG;
   const int nqb = (seq_len + BQ - 1) / BQ;
-  // Balanced pairs (TEAMS = 2) pay off when they make one to two rounds of
-  // 8-wave workgroups on the 256 CUs: fewer pairs leave CUs idle, more
-  // rounds let the dispatcher balance single q blocks by itself.  With
-  // 16-row head groups (HG = 8) the single-block split measured faster.
-  const unsigned pair_blocks = (unsigned)(((nqb + 1) / 2) * Hkv * (G / HG));
-  int teams = pair_blocks >= 256 && pair_blocks <= 512 && HG <= 4 ? 2 : 1;
-  if (const int o = prefill_teams_override(); o == 1 || o == 2) teams = o;
-  const unsigned blocks = teams == 2 ? pair_blocks : (unsigned)(nqb * Hkv * (G / HG));
-#define GROUT_PREFILL_CASE(hg)                                                              \
-  case hg:                                                                                  \
-    if (teams == 2)                                                                         \
-      fmha_prefill_kernel<hg, 2><<<blocks, 512, 0, stream>>>(                              \
-          (const half_t*)q, (const half_t*)k_cache, (const half_t*)v_cache, (half_t*)out,   \
-          seq_len, pos0, Hq, Hkv, head_stride, scale_log2, nqb);                            \
-    else                                                                                    \
-      fmha_prefill_kernel<hg, 1><<<blocks, 256, 0, stream>>>(                              \
-          (const half_t*)q, (const half_t*)k_cache, (const half_t*)v_cache, (half_t*)out,   \
-          seq_len, pos0, Hq, Hkv, head_stride, scale_log2, nqb);                            \
+  const int per_block = Hkv * (G / HG);
+  // Complementary pairs give every workgroup the same work; they are used
+  // when there are enough of them for one workgroup per CU (256 CUs).
+  const long pair_blocks = (long)((nqb + 1) / 2) * per_block;
+  int paired = pair_blocks >= 256 ? 1 : 0;
+  if (const int o = prefill_paired_override(); o == 0 || o == 1) paired = o;
+  const long blocks = (paired ? (nqb + 1) / 2 : nqb) * (long)per_block;
+  if (blocks <= 0 || blocks > 0x7fffffffL) return hipErrorInvalidValue;
+#define GROUT_PREFILL_CASE(hg)                                                            \
+  case hg:                                                                                \
+    fmha_prefill_kernel<hg><<<(unsigned)blocks, 512, 0, stream>>>(                        \
+        (const half_t*)q, (const half_t*)k_cache, (const half_t*)v_cache, (half_t*)out,   \
+        seq_len, pos0, Hq, Hkv, head_stride, scale_log2, nqb, paired);                    \
     break;
   switch (HG) {
     GROUT_PREFILL_CASE(1)

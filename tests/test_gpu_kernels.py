@@ -172,24 +172,45 @@ def test_prefill_attention_vs_oracle(gpu, S, Hq, Hkv, pos0):
     assert_close(host_f32(out), ref, f"prefill S={S} Hq={Hq} Hkv={Hkv} pos0={pos0}")
 
 
-@pytest.mark.parametrize("teams", [1, 2])
+@pytest.mark.parametrize("paired", [0, 1])
 @pytest.mark.parametrize("S,Hq,Hkv,pos0", [
     (1, 32, 8, 0), (17, 32, 8, 0), (130, 64, 8, 0), (200, 32, 8, 77), (77, 40, 8, 9),
-    (33, 16, 1, 0), (700, 32, 8, 100), (1000, 16, 4, 0)])
-def test_prefill_work_splits_vs_oracle(gpu, monkeypatch, teams, S, Hq, Hkv, pos0):
-    """Both work splits of the prefill kernel (one q block per 4-wave
-    workgroup; complementary q-block pairs split over two 4-wave teams with
-    an LDS merge), forced through GROUT_FMHA_PREFILL_TEAMS, on odd block
-    counts, a kv prefix (pos0 > 0) and a single kv head."""
-    monkeypatch.setenv("GROUT_FMHA_PREFILL_TEAMS", str(teams))
-    _say("prefill_split", teams, S, Hq, Hkv, pos0)
+    (33, 16, 1, 0), (700, 32, 8, 100), (1000, 16, 4, 0), (2048, 24, 8, 0)])
+def test_prefill_work_splits_vs_oracle(gpu, monkeypatch, paired, S, Hq, Hkv, pos0):
+    """Both work splits of the prefill kernel (a q block per workgroup, its
+    tiles split over the two 4-wave teams; complementary q-block pairs, team B
+    taking the light block and the tail of the heavy one), forced through
+    GROUT_FMHA_PREFILL_PAIRED, on odd block counts, a kv prefix (pos0 > 0), a
+    single kv head and HG = 3 (rows that fall outside a 126-row block)."""
+    monkeypatch.setenv("GROUT_FMHA_PREFILL_PAIRED", str(paired))
+    _say("prefill_split", paired, S, Hq, Hkv, pos0)
     max_ctx = pos0 + S + 3
     q = normal(f"wq{S}", (S, Hq, D))
     kc, vc = normal(f"wk{S}", (Hkv, max_ctx, D)), normal(f"wv{S}", (Hkv, max_ctx, D))
+    rows = None if S <= 1000 else np.r_[0:64, 700:764, S - 64:S]
+    ref = O.attention_prefill_rows(q, kc, vc, pos0, rows=rows, nthreads=16)
+    out = gpu.ops.fmha_prefill(dev(q), dev(kc), dev(vc), pos0)
+    torch.cuda.synchronize()
+    got = host_f32(out) if rows is None else host_f32(out)[rows]
+    assert_close(got, ref, f"prefill paired={paired} S={S} Hq={Hq} Hkv={Hkv} pos0={pos0}")
+
+
+@pytest.mark.parametrize("S,pos0", [(77, 0), (130, 61), (1000, 24)])
+def test_prefill_ignores_cache_rows_past_kv_len(gpu, S, pos0):
+    """Cache rows at and past kv_len = pos0 + S hold NaN: the last kv tile
+    reads them as zeros (bounded loads) and masks them, so outputs stay equal
+    to the oracle's, which never reads them."""
+    _say("prefill_nan_tail", S, pos0)
+    Hq, Hkv, max_ctx = 32, 8, pos0 + S + 70
+    q = normal(f"nt{S}", (S, Hq, D))
+    kc, vc = normal(f"ntk{S}", (Hkv, max_ctx, D)), normal(f"ntv{S}", (Hkv, max_ctx, D))
+    nan16 = np.uint16(0x7E00)
+    kc[:, pos0 + S:] = nan16
+    vc[:, pos0 + S:] = nan16
     ref = O.attention_prefill_rows(q, kc, vc, pos0, nthreads=16)
     out = gpu.ops.fmha_prefill(dev(q), dev(kc), dev(vc), pos0)
     torch.cuda.synchronize()
-    assert_close(host_f32(out), ref, f"prefill teams={teams} S={S} Hq={Hq} Hkv={Hkv} pos0={pos0}")
+    assert_close(host_f32(out), ref, f"prefill nan tail S={S} pos0={pos0}")
 
 
 # ------------------------------------------------------- configs end to end
