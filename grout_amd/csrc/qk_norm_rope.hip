@@ -10,7 +10,9 @@
 // Layout of the work: one row (one head of one token, D = 128 halves = 256 B)
 // per 32 lanes; lane j owns elements 4j..4j+3 (one 8-byte load), so a wave
 // moves two contiguous rows per instruction.  Lanes j and j^16 hold the RoPE
-// partners d and d+64.  Eight rows per 256-thread workgroup.
+// partners d and d+64.  Eight row groups per 256-thread workgroup, each taking
+// kRowsPerGroup heads of one token; lane exchanges use v_permlane16_swap and
+// DPP row rotations (no LDS round trip, no integer division).
 //
 // Bit-exact K rows: this file is compiled with -ffp-contract=off, the sum of
 // squares uses the fixed tree (in-lane (a^2+b^2)+(c^2+d^2), then xor butterfly
@@ -40,84 +42,132 @@ __device__ __forceinline__ float rsqrt_det(float v) {
   return (float)y;
 }
 
-template <bool kDecode>
+// Lane exchanges inside one 32-lane row group, on the VALU (no LDS round
+// trip): xor16 swaps the two 16-lane halves, ror(N) reads lane (l+N) mod 16 of
+// the same half.
+__device__ __forceinline__ float xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  // r[0]: odd halves take the even half's value; r[1]: even halves take the odd half's
+  return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+}
+template <int N>
+__device__ __forceinline__ float ror16(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x120 + N, 0xf, 0xf, false));
+}
+
+// Grid (tokens, ceil((Hq+Hkv)/(8R))): 32-lane group g of the 256-thread
+// workgroup takes heads h = 8R*blockIdx.y + g + 8r (r < R) of token
+// blockIdx.x.  The cos/sin row is loaded once per group, every load is issued
+// before any row is computed, and the R rows' reduction and Newton chains are
+// independent, so they overlap.  One row per group measured fastest on MI355X
+// (S=2048, 4B: 13.4 us at R = 1, 14.3 us at R = 5): more, smaller workgroups
+// keep more independent HBM requests in flight.
+constexpr int kRowsPerGroup = 1;
+
+template <bool kDecode, int R>
 __global__ __launch_bounds__(256) void qk_norm_rope_kv_kernel(
     const half_t* __restrict__ q, const half_t* __restrict__ k, const half_t* __restrict__ v,
     const half_t* __restrict__ gamma_q, const half_t* __restrict__ gamma_k,
     const float* __restrict__ rope_cos, const float* __restrict__ rope_sin,
     half_t* __restrict__ q_out, half_t* __restrict__ k_cache, half_t* __restrict__ v_cache,
-    const uint32_t* __restrict__ d_pos, int pos0, int seq_len, int Hq, int Hkv,
-    long head_stride, int max_ctx, float eps) {
-  const int H = Hq + Hkv;
-  const int row = blockIdx.x * 8 + (threadIdx.x >> 5);
+    const uint32_t* __restrict__ d_pos, int pos0, int Hq, int Hkv, long head_stride,
+    int max_ctx, float eps) {
+  const int s = blockIdx.x;
+  const int h0 = blockIdx.y * 8 * R + (threadIdx.x >> 5);
   const int j = threadIdx.x & 31;
-  if (row >= seq_len * H) return;  // uniform across the 32 lanes of a row
-  const int s = row / H;
-  const int h = row - s * H;
+  const int H = Hq + Hkv;
+  if (h0 >= H) return;  // uniform across the 32 lanes of a row group
   const int pos = kDecode ? (int)d_pos[0] : pos0 + s;
   if (pos < 0 || pos >= max_ctx) return;  // never write outside the cache
-  const bool is_q = h < Hq;
-  const int kvh = h - Hq;
 
-  const half_t* x;
-  if (kDecode) {
-    x = q + (size_t)h * kHeadDim;  // qkv = [Q | K | V], K rows follow Q rows
-  } else {
-    x = is_q ? q + ((size_t)s * Hq + h) * kHeadDim : k + ((size_t)s * Hkv + kvh) * kHeadDim;
-  }
-  const u32x2 xr = *reinterpret_cast<const u32x2*>(x + 4 * j);
-  const half4 xh = __builtin_bit_cast(half4, xr);
-  const float x0 = (float)xh[0], x1 = (float)xh[1], x2 = (float)xh[2], x3 = (float)xh[3];
-
-  // Sum of squares: fixed tree.
-  float a0 = x0 * x0, a1 = x1 * x1, a2 = x2 * x2, a3 = x3 * x3;
-  float s0 = a0 + a1, s1 = a2 + a3;
-  float ss = s0 + s1;
-#pragma unroll
-  for (int off = 16; off >= 1; off >>= 1) ss = ss + __shfl_xor(ss, off, 64);
-  const float mean = ss / (float)kHeadDim;
-  const float inv = rsqrt_det(mean + eps);
-
-  const half_t* g = is_q ? gamma_q : gamma_k;
-  const half4 gh = __builtin_bit_cast(half4, *reinterpret_cast<const u32x2*>(g + 4 * j));
-  float n[4];
-  n[0] = (x0 * inv) * (float)gh[0];
-  n[1] = (x1 * inv) * (float)gh[1];
-  n[2] = (x2 * inv) * (float)gh[2];
-  n[3] = (x3 * inv) * (float)gh[3];
-  float p[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) p[i] = __shfl_xor(n[i], 16, 64);  // RoPE partner (d +/- 64)
-
+  // All loads first.
   const size_t trow = (size_t)pos * (kHeadDim / 2) + 4 * (j & 15);
   const floatx4 c = *reinterpret_cast<const floatx4*>(rope_cos + trow);
   const floatx4 sn = *reinterpret_cast<const floatx4*>(rope_sin + trow);
-  half4 y;
-  if (j < 16) {  // low half: y = n_lo*c - n_hi*s
+  const half4 gq = __builtin_bit_cast(half4, *reinterpret_cast<const u32x2*>(gamma_q + 4 * j));
+  const half4 gk = __builtin_bit_cast(half4, *reinterpret_cast<const u32x2*>(gamma_k + 4 * j));
+  u32x2 xr[R], vr[R];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float t0 = n[i] * c[i];
-      float t1 = p[i] * sn[i];
-      y[i] = (half_t)(t0 - t1);
+  for (int r = 0; r < R; ++r) {
+    const int h = h0 + 8 * r;
+    xr[r] = u32x2{0u, 0u};
+    vr[r] = u32x2{0u, 0u};
+    if (h >= H) continue;
+    const bool is_q = h < Hq;
+    const int kvh = h - Hq;
+    const half_t* x;
+    if (kDecode) {
+      x = q + (size_t)h * kHeadDim;  // qkv = [Q | K | V], K rows follow Q rows
+    } else {
+      x = is_q ? q + ((size_t)s * Hq + h) * kHeadDim : k + ((size_t)s * Hkv + kvh) * kHeadDim;
     }
-  } else {  // high half: y = n_hi*c + n_lo*s
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float t0 = n[i] * c[i];
-      float t1 = p[i] * sn[i];
-      y[i] = (half_t)(t0 + t1);
+    xr[r] = *reinterpret_cast<const u32x2*>(x + 4 * j);
+    if (!is_q) {
+      const half_t* vrow = kDecode ? v + (size_t)(Hq + Hkv + kvh) * kHeadDim
+                                   : v + ((size_t)s * Hkv + kvh) * kHeadDim;
+      vr[r] = *reinterpret_cast<const u32x2*>(vrow + 4 * j);
     }
   }
-  const u32x2 yr = __builtin_bit_cast(u32x2, y);
-  if (is_q) {
-    half_t* dst = kDecode ? q_out + (size_t)h * kHeadDim : q_out + ((size_t)s * Hq + h) * kHeadDim;
-    *reinterpret_cast<u32x2*>(dst + 4 * j) = yr;
-  } else {
-    const size_t coff = (size_t)kvh * head_stride + (size_t)pos * kHeadDim + 4 * j;
-    *reinterpret_cast<u32x2*>(k_cache + coff) = yr;
-    const half_t* vrow = kDecode ? v + (size_t)(Hq + Hkv + kvh) * kHeadDim
-                                 : v + ((size_t)s * Hkv + kvh) * kHeadDim;
-    *reinterpret_cast<u32x2*>(v_cache + coff) = *reinterpret_cast<const u32x2*>(vrow + 4 * j);
+
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int h = h0 + 8 * r;
+    if (h >= H) continue;  // uniform across the group
+    const bool is_q = h < Hq;
+    const int kvh = h - Hq;
+    const half4 xh = __builtin_bit_cast(half4, xr[r]);
+    const float x0 = (float)xh[0], x1 = (float)xh[1], x2 = (float)xh[2], x3 = (float)xh[3];
+
+    // Sum of squares: fixed tree, in-lane (a^2+b^2)+(c^2+d^2) then the
+    // butterfly over partners l^16, l^8, l^4, l^2, l^1.  After the l^16 and
+    // l^8 steps lanes l and l^8 hold equal values, so the rotation partners
+    // (l+-4, l+-2, l+-1 mod 16) add exactly the values the xor partners would.
+    float a0 = x0 * x0, a1 = x1 * x1, a2 = x2 * x2, a3 = x3 * x3;
+    float s0 = a0 + a1, s1 = a2 + a3;
+    float ss = s0 + s1;
+    ss = ss + xor16(ss);
+    ss = ss + ror16<8>(ss);
+    ss = ss + ror16<4>(ss);
+    ss = ss + ror16<2>(ss);
+    ss = ss + ror16<1>(ss);
+    const float mean = ss / (float)kHeadDim;
+    const float inv = rsqrt_det(mean + eps);
+
+    const half4 gh = is_q ? gq : gk;
+    float n[4];
+    n[0] = (x0 * inv) * (float)gh[0];
+    n[1] = (x1 * inv) * (float)gh[1];
+    n[2] = (x2 * inv) * (float)gh[2];
+    n[3] = (x3 * inv) * (float)gh[3];
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = xor16(n[i]);  // RoPE partner (d +/- 64)
+
+    half4 y;
+    if (j < 16) {  // low half: y = n_lo*c - n_hi*s
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float t0 = n[i] * c[i];
+        float t1 = p[i] * sn[i];
+        y[i] = (half_t)(t0 - t1);
+      }
+    } else {  // high half: y = n_hi*c + n_lo*s
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float t0 = n[i] * c[i];
+        float t1 = p[i] * sn[i];
+        y[i] = (half_t)(t0 + t1);
+      }
+    }
+    const u32x2 yr = __builtin_bit_cast(u32x2, y);
+    if (is_q) {
+      half_t* dst = kDecode ? q_out + (size_t)h * kHeadDim : q_out + ((size_t)s * Hq + h) * kHeadDim;
+      *reinterpret_cast<u32x2*>(dst + 4 * j) = yr;
+    } else {
+      const size_t coff = (size_t)kvh * head_stride + (size_t)pos * kHeadDim + 4 * j;
+      *reinterpret_cast<u32x2*>(k_cache + coff) = yr;
+      *reinterpret_cast<u32x2*>(v_cache + coff) = vr[r];
+    }
   }
 }
 
@@ -127,12 +177,11 @@ hipError_t launch_qk_norm_rope_kv_prefill(const void* q, const void* k, const vo
                                           void* q_out, void* k_cache, void* v_cache, int pos0,
                                           int seq_len, int Hq, int Hkv, long head_stride,
                                           int max_ctx, float eps, hipStream_t stream) {
-  const long rows = (long)seq_len * (Hq + Hkv);
-  const unsigned blocks = (unsigned)((rows + 7) / 8);
-  qk_norm_rope_kv_kernel<false><<<blocks, 256, 0, stream>>>(
+  const dim3 grid((unsigned)seq_len, (unsigned)((Hq + Hkv + 8 * kRowsPerGroup - 1) / (8 * kRowsPerGroup)));
+  qk_norm_rope_kv_kernel<false, kRowsPerGroup><<<grid, 256, 0, stream>>>(
       (const half_t*)q, (const half_t*)k, (const half_t*)v, (const half_t*)gamma_q,
       (const half_t*)gamma_k, rope_cos, rope_sin, (half_t*)q_out, (half_t*)k_cache,
-      (half_t*)v_cache, nullptr, pos0, seq_len, Hq, Hkv, head_stride, max_ctx, eps);
+      (half_t*)v_cache, nullptr, pos0, Hq, Hkv, head_stride, max_ctx, eps);
   return hipGetLastError();
 }
 
@@ -142,11 +191,11 @@ hipError_t launch_qk_norm_rope_kv_decode(const void* qkv, const void* gamma_q,
                                          void* v_cache, const uint32_t* d_pos, int Hq, int Hkv,
                                          long head_stride, int max_ctx, float eps,
                                          hipStream_t stream) {
-  const unsigned blocks = (unsigned)((Hq + Hkv + 7) / 8);
-  qk_norm_rope_kv_kernel<true><<<blocks, 256, 0, stream>>>(
+  const dim3 grid(1u, (unsigned)((Hq + Hkv + 7) / 8));
+  qk_norm_rope_kv_kernel<true, 1><<<grid, 256, 0, stream>>>(
       (const half_t*)qkv, nullptr, (const half_t*)qkv, (const half_t*)gamma_q,
       (const half_t*)gamma_k, rope_cos, rope_sin, (half_t*)q_out, (half_t*)k_cache,
-      (half_t*)v_cache, d_pos, 0, 1, Hq, Hkv, head_stride, max_ctx, eps);
+      (half_t*)v_cache, d_pos, 0, Hq, Hkv, head_stride, max_ctx, eps);
   return hipGetLastError();
 }
 
