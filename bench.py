@@ -35,7 +35,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--only", default="", help="comma list: decode32b,prefill,decode4b,norm")
+    ap.add_argument("--only", default="",
+                    help="comma list: decode32b,prefill,decode4b,norm,engine4b")
     ap.add_argument("--eager", action="store_true",
                     help="launch the timed calls from the host instead of replaying a captured "
                          "graph (for per-dispatch counter collection)")
@@ -187,6 +188,45 @@ def bench_norm(ops, S, Hq, Hkv, max_ctx, steps, warmup):
     return dict(ms=ms, alg_bytes=alg_bytes)
 
 
+def bench_engine(prompt_len=512, decode_steps=256, max_ctx=1024):
+    """Config 5: Qwen3-4B-shaped engine, random N(0, 0.02) fp16 weights (norm
+    weights 1), a seeded uniform prompt prefilled, then greedy decode steps,
+    each one replay of the captured decode-step graph plus the 4-byte token
+    read-back (the public decode_greedy call, timed on the host clock)."""
+    import numpy as np
+    import torch
+    from grout_amd.model import Engine, Qwen3Config, Qwen3Weights
+
+    cfg = Qwen3Config.qwen3_4b()
+    w = Qwen3Weights.random(cfg, seed=0)
+    eng = Engine(cfg, w, max_ctx=max_ctx)
+    prompt = np.random.default_rng(512).integers(0, cfg.vocab_size, prompt_len)
+    eng.warmup()
+    tok = eng.prefill_greedy(prompt)  # untimed: first rocBLAS calls pick their kernels
+    for _ in range(8):
+        tok = eng.decode_greedy(tok)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    tok = eng.prefill_greedy(prompt)
+    prefill_s = time.perf_counter() - t0
+    toks = [tok]
+    t0 = time.perf_counter()
+    for _ in range(decode_steps):
+        toks.append(eng.decode_greedy(toks[-1]))
+    decode_s = time.perf_counter() - t0
+    eng.close()
+    # per decode token: every fp16 weight once (the tied embedding is read as
+    # the lm_head; the embedding gather is one row) + K and V of the live context
+    weight_bytes = 2 * cfg.num_params()
+    mean_ctx = prompt_len + decode_steps / 2
+    kv_bytes = cfg.num_layers * 2 * cfg.num_key_value_heads * mean_ctx * D * 2
+    del w, eng
+    torch.cuda.empty_cache()
+    return dict(prefill_ms=prefill_s * 1e3, decode_ms=decode_s * 1e3 / decode_steps,
+                tok_s=decode_steps / decode_s, bytes_per_token=weight_bytes + kv_bytes,
+                distinct_tokens=len(set(toks)), mean_ctx=mean_ctx)
+
+
 def cpu_baseline_decode(Hq, Hkv, ctx):
     """Scalar fp32 oracle (single thread) on one 32B decode layer: 16 of the 64
     query heads (2 kv heads) at full context; GB/s scaled to the whole layer."""
@@ -254,6 +294,14 @@ def main():
     if want("norm"):
         res["norm"] = bench_norm(ops, 2048, 32, 8, 32768, a.steps, a.warmup)
         print(f"# norm {res['norm']}", file=sys.stderr, flush=True)
+    if want("engine4b"):
+        res["engine4b"] = bench_engine()
+        # attention part of one decode step at the mean context of the run:
+        # the 36-layer graph of norm/RoPE/KV write + split + merge
+        res["engine4b"]["attn_graph_ms"] = bench_decode_graph(
+            grout_amd, 32, 8, int(res["engine4b"]["mean_ctx"]), 1024, 36,
+            max(a.steps // 4, 10), a.warmup)
+        print(f"# engine4b {res['engine4b']}", file=sys.stderr, flush=True)
 
     line = {"metric": "decode-attn HBM GB/s (% of peak) + prefill FMHA TFLOP/s (% MFMA peak)",
             "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "higher_is_better": True,
@@ -293,6 +341,17 @@ def main():
         line["qk_norm_rope_kv"] = {"workload": "fused QK-norm/RoPE/KV write S=2048 Hq=32 Hkv=8",
                                    "us": round(r["ms"] * 1e3, 2), "gbs": round(gbs, 1),
                                    "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    if "engine4b" in res:
+        r = res["engine4b"]
+        gbs = r["bytes_per_token"] * r["tok_s"] / 1e9
+        line["engine4b"] = {
+            "workload": "qwen3-4b engine, random N(0,0.02) fp16 weights, 512-token prompt, "
+                        "256 greedy decode steps (decode-step hipGraph)",
+            "decode_tok_s": round(r["tok_s"], 1), "decode_ms_per_token": round(r["decode_ms"], 4),
+            "prefill_512_ms": round(r["prefill_ms"], 2),
+            "weight_stream_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "attention_share": round(r["attn_graph_ms"] / r["decode_ms"], 4),
+            "attention_us_per_token": round(r["attn_graph_ms"] * 1e3, 1)}
     if not a.no_cpu and "decode32b" in res:
         cb = cpu_baseline_decode(64, 8, 32768)
         line["cpu_baseline"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in cb.items()}

@@ -31,7 +31,24 @@ class DecodeLayer(C.Structure):
                 ("k_cache", _p), ("v_cache", _p), ("attn_out", _p)]
 
 
-# name -> (restype, argtypes).  Every symbol declared in include/grout_attn.h.
+class Qwen3Config(C.Structure):
+    _fields_ = [("num_layers", _i), ("hidden_size", _i), ("intermediate_size", _i),
+                ("num_q_heads", _i), ("num_kv_heads", _i), ("head_dim", _i), ("vocab_size", _i),
+                ("rms_norm_eps", _f), ("rope_theta", _f), ("max_ctx", _i)]
+
+
+class Qwen3Layer(C.Structure):
+    _fields_ = [("input_layernorm", _p), ("qkv_proj", _p), ("q_norm", _p), ("k_norm", _p),
+                ("o_proj", _p), ("post_attention_layernorm", _p), ("gate_up_proj", _p),
+                ("down_proj", _p)]
+
+
+class Qwen3Weights(C.Structure):
+    _fields_ = [("embed_tokens", _p), ("norm", _p), ("lm_head", _p),
+                ("layers", C.POINTER(Qwen3Layer))]
+
+
+# name -> (restype, argtypes).  Every symbol declared in include/*.h.
 SIGNATURES = {
     "grout_last_error": (C.c_char_p, []),
     "grout_abi_version": (_i, []),
@@ -53,6 +70,22 @@ SIGNATURES = {
     "grout_decode_graph_position_ptr": (_p, [_p]),
     "grout_decode_graph_destroy": (_i, [_p]),
     "grout_diag_mfma_layout": (_i, [_p, _p]),
+    # include/grout_engine.h
+    "grout_embedding": (_i, [_p, _p, _p, _i, _i, _i, _p]),
+    "grout_rms_norm": (_i, [_p, _p, _p, _i, _i, _f, _p]),
+    "grout_add_rms_norm": (_i, [_p, _p, _p, _p, _p, _i, _i, _f, _p]),
+    "grout_silu_mul": (_i, [_p, _p, _i, _i, _p]),
+    "grout_gemv": (_i, [_p, _p, _p, _i, _i, _p]),
+    "grout_argmax_workspace_bytes": (_sz, [_i]),
+    "grout_argmax": (_i, [_p, _i, _p, _sz, _p, _p]),
+    "grout_engine_create": (_i, [C.POINTER(Qwen3Config), C.POINTER(Qwen3Weights), _i,
+                                 C.POINTER(_p)]),
+    "grout_engine_prefill": (_i, [_p, _p, _i, _p, _p]),
+    "grout_engine_decode": (_i, [_p, _u32, _p]),
+    "grout_engine_decode_greedy": (_i, [_p, _u32, _p]),
+    "grout_engine_reset": (_i, [_p]),
+    "grout_engine_position": (_i, [_p]),
+    "grout_engine_destroy": (_i, [_p]),
 }
 
 

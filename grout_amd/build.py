@@ -29,8 +29,12 @@ SOURCES = [
     ("qk_norm_rope.hip", ["-ffp-contract=off"]),
     ("attn_decode.hip", []),
     ("attn_prefill.hip", []),
+    ("model_kernels.hip", []),
     ("api.cpp", ["-x", "hip"]),
+    ("engine.cpp", ["-x", "hip"]),
 ]
+# Prefill projections are plain GEMMs: rocBLAS.
+LIBS = ["-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"]
 
 
 def hipcc() -> str:
@@ -62,7 +66,7 @@ def build(verbose: bool = False, resource_usage: bool = False) -> str:
     with cf.ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
         objs = list(ex.map(lambda s: _compile(s[0], s[1], resource_usage, verbose), SOURCES))
     tmp = LIB + ".tmp"
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, *LIBS, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -34,6 +34,18 @@ hipError_t launch_fmha_prefill(const void* q, const void* k_cache, const void* v
                                void* out, int seq_len, int pos0, int Hq, int Hkv,
                                long head_stride, float qk_scale, hipStream_t stream);
 
+// Model-step kernels (model_kernels.hip).  residual == nullptr selects plain
+// RMSNorm; otherwise out = norm(residual + x), residual_out = residual + x.
+hipError_t launch_embedding(const uint32_t* ids, const void* table, void* out, int rows, int H,
+                            int vocab, hipStream_t stream);
+hipError_t launch_rms_norm(const void* residual, const void* x, const void* w, void* out,
+                           void* residual_out, int rows, int H, float eps, hipStream_t stream);
+hipError_t launch_silu_mul(const void* gate_up, void* out, int rows, int I, hipStream_t stream);
+hipError_t launch_gemv(const void* W, const void* x, void* y, int N, int K, hipStream_t stream);
+int argmax_num_blocks(int V);
+hipError_t launch_argmax(const void* logits, float* block_max, uint32_t* block_idx, int V,
+                         uint32_t* out, hipStream_t stream);
+
 // Writes the 16x16 C fragment of A x B for A[i][k] = i*32+k (k < 32), B = I
 // padded, one float per (lane, element): used to confirm the MFMA lane layout.
 hipError_t launch_mfma_layout_probe(float* out64x4, hipStream_t stream);

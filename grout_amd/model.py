@@ -1,0 +1,259 @@
+"""Qwen3 engine on one MI355X: the Python face of include/grout_engine.h.
+
+Mirrors the reference's public API `grout::Engine` (src/api.rs:11-183):
+token-based and blocking; `prefill` starts a new session and returns the last
+token's logits, `decode` / `decode_greedy` advance it one token through the
+captured decode-step HIP graph, `reset` clears the KV state.  Weights are
+fp16 device tensors in the reference's fused layouts (qkv_proj rows
+[Q | K | V], gate_up_proj rows [gate | up]); the engine borrows them, so this
+object keeps references to them for its lifetime.
+
+All compute runs in grout_amd/libgrout_attn.so; nothing here falls back to
+PyTorch math.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Sequence
+
+import numpy as np
+import torch
+
+from ._lib import Qwen3Config as _CConfig
+from ._lib import Qwen3Layer as _CLayer
+from ._lib import Qwen3Weights as _CWeights
+from ._lib import call, lib
+
+HEAD_DIM = 128
+LAYER_KEYS = ("input_layernorm", "qkv_proj", "q_norm", "k_norm", "o_proj",
+              "post_attention_layernorm", "gate_up_proj", "down_proj")
+
+
+@dataclass(frozen=True)
+class Qwen3Config:
+    """The Qwen3Config fields the engine reads (src/config.rs:7-33)."""
+    num_layers: int
+    hidden_size: int
+    intermediate_size: int
+    num_attention_heads: int
+    num_key_value_heads: int
+    vocab_size: int
+    head_dim: int = HEAD_DIM
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 1e6
+    tie_word_embeddings: bool = True
+    eos_token_ids: tuple = (151645, 151643)
+
+    @staticmethod
+    def qwen3_4b() -> "Qwen3Config":
+        """Qwen3-4B: 36 layers, hidden 2560, inter 9728, 32/8 heads, vocab 151936."""
+        return Qwen3Config(36, 2560, 9728, 32, 8, 151936)
+
+    @property
+    def q_dim(self) -> int:
+        return self.num_attention_heads * self.head_dim
+
+    @property
+    def kv_dim(self) -> int:
+        return self.num_key_value_heads * self.head_dim
+
+    def layer_shapes(self) -> Dict[str, tuple]:
+        H, I = self.hidden_size, self.intermediate_size
+        return {
+            "input_layernorm": (H,),
+            "qkv_proj": (self.q_dim + 2 * self.kv_dim, H),
+            "q_norm": (self.head_dim,),
+            "k_norm": (self.head_dim,),
+            "o_proj": (H, self.q_dim),
+            "post_attention_layernorm": (H,),
+            "gate_up_proj": (2 * I, H),
+            "down_proj": (H, I),
+        }
+
+    def num_params(self) -> int:
+        per_layer = sum(math.prod(s) for s in self.layer_shapes().values())
+        embed = self.vocab_size * self.hidden_size
+        head = 0 if self.tie_word_embeddings else embed
+        return self.num_layers * per_layer + embed + head + self.hidden_size
+
+
+@dataclass
+class Qwen3Weights:
+    """fp16 device tensors: embed_tokens [V][H], norm [H], lm_head (the
+    embedding when tied) and one dict of LAYER_KEYS tensors per layer."""
+    embed_tokens: torch.Tensor
+    norm: torch.Tensor
+    layers: List[Dict[str, torch.Tensor]]
+    lm_head: Optional[torch.Tensor] = None
+
+    def head(self) -> torch.Tensor:
+        return self.embed_tokens if self.lm_head is None else self.lm_head
+
+    @staticmethod
+    def random(cfg: Qwen3Config, seed: int = 0, device="cuda", std: float = 0.02,
+               norm_value: float = 1.0) -> "Qwen3Weights":
+        """Matrices ~ N(0, std) drawn on the device, norm weights = norm_value."""
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+
+        def mat(shape):
+            t = torch.empty(shape, dtype=torch.float16, device=device)
+            t.normal_(0.0, std, generator=g)
+            return t
+
+        def vec(n):
+            return torch.full((n,), norm_value, dtype=torch.float16, device=device)
+
+        layers = []
+        for _ in range(cfg.num_layers):
+            layer = {}
+            for k, shp in cfg.layer_shapes().items():
+                layer[k] = vec(shp[0]) if len(shp) == 1 else mat(shp)
+            layers.append(layer)
+        embed = mat((cfg.vocab_size, cfg.hidden_size))
+        head = None if cfg.tie_word_embeddings else mat((cfg.vocab_size, cfg.hidden_size))
+        return Qwen3Weights(embed, vec(cfg.hidden_size), layers, head)
+
+    @staticmethod
+    def from_host(host: dict, device="cuda") -> "Qwen3Weights":
+        """From numpy fp16 bit patterns (uint16) in the same structure."""
+        def dev(a):
+            return torch.from_numpy(np.ascontiguousarray(a).view(np.float16)).to(device)
+
+        layers = [{k: dev(v) for k, v in L.items()} for L in host["layers"]]
+        head = host.get("lm_head")
+        return Qwen3Weights(dev(host["embed_tokens"]), dev(host["norm"]), layers,
+                            None if head is None else dev(head))
+
+    def check(self, cfg: Qwen3Config) -> None:
+        def need(t, shape, what):
+            if tuple(t.shape) != tuple(shape) or t.dtype != torch.float16 or not t.is_cuda \
+                    or not t.is_contiguous():
+                raise ValueError(f"{what}: expected contiguous fp16 cuda {shape}, got "
+                                 f"{t.dtype} {tuple(t.shape)} on {t.device}")
+
+        need(self.embed_tokens, (cfg.vocab_size, cfg.hidden_size), "embed_tokens")
+        need(self.norm, (cfg.hidden_size,), "norm")
+        need(self.head(), (cfg.vocab_size, cfg.hidden_size), "lm_head")
+        if len(self.layers) != cfg.num_layers:
+            raise ValueError(f"{len(self.layers)} layers, config has {cfg.num_layers}")
+        for i, L in enumerate(self.layers):
+            for k, shp in cfg.layer_shapes().items():
+                need(L[k], shp, f"layer {i} {k}")
+
+
+@dataclass
+class Logits:
+    """Last-token logits copied to the host as f32 (src/api.rs:39-44)."""
+    values: np.ndarray
+
+
+@dataclass(frozen=True)
+class ModelMeta:
+    """src/api.rs:46-57."""
+    vocab_size: int
+    eos_token_ids: tuple
+    arch: str
+    max_ctx: int
+
+
+class Engine:
+    """Synchronous Qwen3 engine (src/api.rs:11-183) over the C ABI."""
+
+    def __init__(self, cfg: Qwen3Config, weights: Qwen3Weights, max_ctx: int = 4096,
+                 device_ord: int = 0):
+        if max_ctx <= 0:
+            raise ValueError("max_ctx must be positive")
+        weights.check(cfg)
+        self.cfg = cfg
+        self.weights = weights  # borrowed by the engine: keep alive
+        self._meta = ModelMeta(cfg.vocab_size, tuple(cfg.eos_token_ids), "qwen3", max_ctx)
+        c = _CConfig(cfg.num_layers, cfg.hidden_size, cfg.intermediate_size,
+                     cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim,
+                     cfg.vocab_size, cfg.rms_norm_eps, cfg.rope_theta, max_ctx)
+        self._layers = (_CLayer * cfg.num_layers)()
+        for i, L in enumerate(weights.layers):
+            for k in LAYER_KEYS:
+                setattr(self._layers[i], k, L[k].data_ptr())
+        w = _CWeights(weights.embed_tokens.data_ptr(), weights.norm.data_ptr(),
+                      weights.head().data_ptr(), self._layers)
+        self._h = C.c_void_p()
+        call("grout_engine_create", C.byref(c), C.byref(w), device_ord, C.byref(self._h))
+        self._logits = np.empty(cfg.vocab_size, np.float32)
+
+    # -- src/api.rs:92-108
+    def prefill(self, tokens: Sequence[int]) -> Logits:
+        ids = np.ascontiguousarray(np.asarray(tokens, dtype=np.int64), dtype=np.uint32)
+        if ids.ndim != 1 or ids.size == 0:
+            raise ValueError("prefill requires at least one token")
+        out = np.empty(self.cfg.vocab_size, np.float32)
+        call("grout_engine_prefill", self._h, ids.ctypes.data_as(C.c_void_p), ids.size,
+             out.ctypes.data_as(C.c_void_p), None)
+        return Logits(out)
+
+    def prefill_greedy(self, tokens: Sequence[int]) -> int:
+        """Prefill and return the greedy next token (device argmax only)."""
+        ids = np.ascontiguousarray(np.asarray(tokens, dtype=np.int64), dtype=np.uint32)
+        if ids.ndim != 1 or ids.size == 0:
+            raise ValueError("prefill requires at least one token")
+        tok = C.c_uint32()
+        call("grout_engine_prefill", self._h, ids.ctypes.data_as(C.c_void_p), ids.size, None,
+             C.byref(tok))
+        return int(tok.value)
+
+    # -- src/api.rs:110-121
+    def decode(self, token: int) -> Logits:
+        out = np.empty(self.cfg.vocab_size, np.float32)
+        call("grout_engine_decode", self._h, int(token), out.ctypes.data_as(C.c_void_p))
+        return Logits(out)
+
+    # -- src/api.rs:123-137
+    def decode_greedy(self, token: int) -> int:
+        tok = C.c_uint32()
+        call("grout_engine_decode_greedy", self._h, int(token), C.byref(tok))
+        return int(tok.value)
+
+    # -- src/api.rs:139-154
+    def reset(self) -> None:
+        call("grout_engine_reset", self._h)
+
+    def meta(self) -> ModelMeta:
+        return self._meta
+
+    @property
+    def position(self) -> int:
+        return int(lib().grout_engine_position(self._h))
+
+    # -- src/api.rs:162-170
+    def warmup(self) -> None:
+        tok = self._meta.eos_token_ids[0] if self._meta.eos_token_ids else 0
+        tok = tok if tok < self.cfg.vocab_size else 0
+        self.prefill_greedy([tok])
+        self.decode_greedy(tok)
+        self.reset()
+
+    def generate_greedy(self, prompt: Sequence[int], max_new_tokens: int) -> List[int]:
+        """Prefill, then greedy decode: returns the max_new_tokens generated ids."""
+        out = [self.prefill_greedy(prompt)]
+        while len(out) < max_new_tokens:
+            out.append(self.decode_greedy(out[-1]))
+        return out[:max_new_tokens]
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) and self._h.value:
+            lib().grout_engine_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()

@@ -1,0 +1,157 @@
+/*
+ * grout_engine.h -- C ABI of the Qwen3 decode/prefill engine built around the
+ * gfx950 attention path of grout_attn.h (one GPU, fp16 weights).
+ *
+ * It replaces the reference's public Rust API `grout::Engine`
+ * (src/api.rs:11-183) over Qwen3Engine (src/model.rs): a synchronous,
+ * token-based engine.  Conventions are those of grout_attn.h (status codes,
+ * grout_last_error()), with these differences:
+ *  - The engine owns its KV caches, activation buffers, RoPE tables, one HIP
+ *    stream, a rocBLAS handle (prefill GEMMs) and the captured decode-step
+ *    HIP graph.  It borrows the weights: every weight pointer is caller-owned
+ *    device memory that must stay valid until grout_engine_destroy.
+ *  - Calls are blocking (they synchronize the engine's stream before
+ *    returning, like Engine's block_on in src/api.rs:97-126) and must not be
+ *    made concurrently on one engine.
+ *  - Weight layouts are the reference's fused ones (src/model.rs weights):
+ *    qkv_proj rows [Q (Hq*128) | K (Hkv*128) | V (Hkv*128)] x hidden,
+ *    gate_up_proj rows [gate (inter) | up (inter)] x hidden, every matrix
+ *    row-major [out_features][in_features] fp16, 16-byte aligned.
+ */
+#ifndef GROUT_ENGINE_H
+#define GROUT_ENGINE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "grout_attn.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GROUT_EBLAS (-4) /* a rocBLAS call of the prefill failed (message in grout_last_error) */
+
+/* The Qwen3Config fields the engine reads (src/config.rs:7-33). */
+typedef struct grout_qwen3_config {
+  int num_layers;           /* num_hidden_layers */
+  int hidden_size;          /* multiple of 8, at most 8192 */
+  int intermediate_size;    /* multiple of 8 */
+  int num_q_heads;          /* num_attention_heads */
+  int num_kv_heads;         /* num_key_value_heads; Hq/Hkv <= 16 */
+  int head_dim;             /* must be 128 */
+  int vocab_size;
+  float rms_norm_eps;       /* 1e-6 for Qwen3 */
+  float rope_theta;         /* 1e6 for Qwen3 */
+  int max_ctx;              /* allocated context (KV cache rows per layer) */
+} grout_qwen3_config;
+
+/* One decoder layer's weights (borrowed device pointers, fp16). */
+typedef struct grout_qwen3_layer {
+  const void* input_layernorm;           /* [hidden] */
+  const void* qkv_proj;                  /* [(Hq+2Hkv)*128][hidden] */
+  const void* q_norm;                    /* [128] */
+  const void* k_norm;                    /* [128] */
+  const void* o_proj;                    /* [hidden][Hq*128] */
+  const void* post_attention_layernorm;  /* [hidden] */
+  const void* gate_up_proj;              /* [2*inter][hidden] */
+  const void* down_proj;                 /* [hidden][inter] */
+} grout_qwen3_layer;
+
+typedef struct grout_qwen3_weights {
+  const void* embed_tokens;         /* [vocab][hidden] */
+  const void* norm;                 /* [hidden], the final norm */
+  const void* lm_head;              /* [vocab][hidden]; == embed_tokens when tied */
+  const grout_qwen3_layer* layers;  /* num_layers entries (the array is copied) */
+} grout_qwen3_weights;
+
+/* ------------------------------------------------------------------ */
+/* Step kernels around the attention path (device pointers, async on   */
+/* `stream`, graph-capturable; fp16 rows of `hidden` elements)          */
+/* ------------------------------------------------------------------ */
+
+/* out[r] = table[ids[r]] for r < rows; ids is device memory (u32).  An id
+ * >= vocab_size gives a zero row (the engine rejects such ids first).
+ * Replaces embedding_f16 / embedding_batch_f16 (src/kernels.rs:1893-1938). */
+int grout_embedding(const uint32_t* ids, const void* table, void* out, int rows, int hidden,
+                    int vocab_size, void* stream);
+
+/* out = f16(x * 1/sqrt(sum(x^2)/hidden + eps) * w) per row, fp32 math.
+ * Replaces rms_norm_f16 (src/kernels.rs:1530-1569). */
+int grout_rms_norm(const void* x, const void* w, void* out, int rows, int hidden, float eps,
+                   void* stream);
+
+/* c = residual + x (fp32); out = f16(c * 1/sqrt(sum(c^2)/hidden + eps) * w);
+ * residual_out = f16(c).  residual_out may alias residual.
+ * Replaces add_rms_norm_decode_raw_f16 (src/kernels.rs:4518-4657). */
+int grout_add_rms_norm(const void* residual, const void* x, const void* w, void* out,
+                       void* residual_out, int rows, int hidden, float eps, void* stream);
+
+/* gate_up rows [gate (inter) | up (inter)] -> out rows f16(silu(gate) * up).
+ * Replaces silu_mul_2d_f16 (src/kernels.rs:1493-1522). */
+int grout_silu_mul(const void* gate_up, void* out, int rows, int inter, void* stream);
+
+/* y[n] = sum_k W[n][k] x[k], W row-major [n][k] fp16, fp32 accumulation,
+ * f16 out; k a multiple of 8.  Replaces the decode GEMVs (cuBLAS in the
+ * reference, src/cublas.rs:434-570). */
+int grout_gemv(const void* W, const void* x, void* y, int n, int k, void* stream);
+
+/* Scratch bytes grout_argmax needs for vocab_size logits. */
+size_t grout_argmax_workspace_bytes(int vocab_size);
+
+/* out[0] = index of the largest of logits[0..vocab_size) (f16), ties to the
+ * smallest index.  Two launches.  Replaces argmax_blocks_f16 +
+ * argmax_reduce_blocks_to_u32 (src/kernels.rs:1571-1740). */
+int grout_argmax(const void* logits, int vocab_size, void* workspace, size_t workspace_bytes,
+                 uint32_t* out, void* stream);
+
+/* ------------------------------------------------------------------ */
+/* Engine                                                              */
+/* ------------------------------------------------------------------ */
+
+typedef struct grout_engine grout_engine;
+
+/* Validates the configuration and every weight pointer, allocates the
+ * engine's device state on `device` and captures the decode-step graph.
+ * Mirrors Engine::load (src/api.rs:60-90) minus the file loading, with the
+ * graph capture of DecodeCudaGraphRunner (src/model.rs:408-596,
+ * 2631-4006). */
+int grout_engine_create(const grout_qwen3_config* config, const grout_qwen3_weights* weights,
+                        int device, grout_engine** out);
+
+/* New-session prefill over tokens[0..n_tokens) (positions 0..n-1).  Writes
+ * the last token's logits as f32 to logits_out (vocab_size floats, host
+ * memory, may be NULL) and its greedy argmax to next_token (may be NULL).
+ * Fails with GROUT_EINVAL for n_tokens < 1, n_tokens > max_ctx or a token
+ * id >= vocab_size.  Mirrors Engine::prefill (src/api.rs:92-108). */
+int grout_engine_prefill(grout_engine* engine, const uint32_t* tokens, int n_tokens,
+                         float* logits_out, uint32_t* next_token);
+
+/* Decodes `token` at the next position of the session (one replay of the
+ * decode-step graph) and writes next-token logits (f32, vocab_size floats).
+ * Requires a preceding prefill and position < max_ctx.
+ * Mirrors Engine::decode (src/api.rs:110-121). */
+int grout_engine_decode(grout_engine* engine, uint32_t token, float* logits_out);
+
+/* As grout_engine_decode, but returns only the greedy next token (device
+ * argmax; 4 bytes cross to the host).  Mirrors Engine::decode_greedy
+ * (src/api.rs:123-137). */
+int grout_engine_decode_greedy(grout_engine* engine, uint32_t token, uint32_t* next_token);
+
+/* Ends the session: the next call must be a prefill.  The KV caches are
+ * zeroed in place (graph pointers stay valid).  A failure is also stashed
+ * and reported by the next call.  Mirrors Engine::reset (src/api.rs:139-154)
+ * and the in-place cache reset (src/model.rs:536-565). */
+int grout_engine_reset(grout_engine* engine);
+
+/* Position the next decode writes (number of tokens in the session). */
+int grout_engine_position(const grout_engine* engine);
+
+/* Frees everything the engine owns (not the weights).  NULL is a no-op. */
+int grout_engine_destroy(grout_engine* engine);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GROUT_ENGINE_H */
