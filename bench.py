@@ -36,7 +36,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--only", default="",
-                    help="comma list: decode32b,prefill,decode4b,norm,engine4b")
+                    help="comma list: decode32b,prefill,decode4b,norm,engine4b (gemv: only "
+                         "when named)")
     ap.add_argument("--eager", action="store_true",
                     help="launch the timed calls from the host instead of replaying a captured "
                          "graph (for per-dispatch counter collection)")
@@ -227,6 +228,52 @@ def bench_engine(prompt_len=512, decode_steps=256, max_ctx=1024):
                 distinct_tokens=len(set(toks)), mean_ctx=mean_ctx)
 
 
+def bench_gemv(steps, warmup):
+    """The decode step's projections on Qwen3-4B shapes, each over 8 rotating
+    weight copies (> the 256 MB Infinity Cache for all but the smallest), as
+    called in the decode graph (fused norm / SiLU inputs included)."""
+    import ctypes as C
+    import torch
+    from grout_amd._lib import call
+
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(3)
+    H, I, QKV, Q, V = 2560, 9728, 6144, 4096, 151936
+    # name: (weight rows, K, mode); gate_up_norm_silu writes I outputs
+    shapes = {"qkv_norm": (QKV, H, "norm"), "o_proj": (H, Q, "plain"),
+              "gate_up_norm_silu": (2 * I, H, "silu"), "down": (H, I, "plain"),
+              "lm_head": (V, H, "plain")}
+    out = {}
+    for name, (n, k, mode) in shapes.items():
+        copies = 1 if name == "lm_head" else 8
+        Ws = [torch.empty((n, k), dtype=torch.float16, device=dev).normal_(0, 0.02, generator=g)
+              for _ in range(copies)]
+        x = torch.randn(2 * k, dtype=torch.float16, device=dev, generator=g)
+        r = torch.randn(k, dtype=torch.float16, device=dev, generator=g)
+        gam = torch.ones(k, dtype=torch.float16, device=dev)
+        ro = torch.empty(k, dtype=torch.float16, device=dev)
+        y = torch.empty(n, dtype=torch.float16, device=dev)
+        P = lambda t: C.c_void_p(t.data_ptr())
+
+        def fn(i, Ws=Ws, x=x, r=r, gam=gam, ro=ro, y=y, n=n, k=k, mode=mode):
+            s = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+            W = P(Ws[i % len(Ws)])
+            if mode == "plain":
+                call("grout_gemv", W, P(x), P(y), n, k, s)
+            elif mode == "norm":
+                call("grout_gemv_rms_norm", W, P(r), P(x), P(gam), P(ro), P(y), n, k,
+                     C.c_float(1e-6), s)
+            else:
+                call("grout_gemv_rms_norm_silu_mul", W, P(r), P(x), P(gam), P(ro), P(y), n // 2,
+                     k, C.c_float(1e-6), s)
+
+        ms = time_launches(fn, steps, warmup)
+        out[name] = dict(us=round(ms * 1e3, 2), gbs=round(n * k * 2 / (ms * 1e-3) / 1e9, 1))
+        del Ws
+        torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline_decode(Hq, Hkv, ctx):
     """Scalar fp32 oracle (single thread) on one 32B decode layer: 16 of the 64
     query heads (2 kv heads) at full context; GB/s scaled to the whole layer."""
@@ -294,6 +341,9 @@ def main():
     if want("norm"):
         res["norm"] = bench_norm(ops, 2048, 32, 8, 32768, a.steps, a.warmup)
         print(f"# norm {res['norm']}", file=sys.stderr, flush=True)
+    if "gemv" in only:
+        res["gemv"] = bench_gemv(a.steps, a.warmup)
+        print(f"# gemv {res['gemv']}", file=sys.stderr, flush=True)
     if want("engine4b"):
         res["engine4b"] = bench_engine()
         # attention part of one decode step at the mean context of the run:
@@ -341,6 +391,8 @@ def main():
         line["qk_norm_rope_kv"] = {"workload": "fused QK-norm/RoPE/KV write S=2048 Hq=32 Hkv=8",
                                    "us": round(r["ms"] * 1e3, 2), "gbs": round(gbs, 1),
                                    "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    if "gemv" in res:
+        line["gemv"] = res["gemv"]
     if "engine4b" in res:
         r = res["engine4b"]
         gbs = r["bytes_per_token"] * r["tok_s"] / 1e9

@@ -55,8 +55,8 @@ struct Arena {
 
 // Decode-step activations: one token.
 struct DecodeBufs {
-  size_t hidden, normed, hidden_after_attn, qkv, q_rope, attn_out, attn_proj, ff_normed, gate_up,
-      ff, ff_down, logits, argmax_max, argmax_idx, token, pos, workspace;
+  size_t hidden, normed, hidden_after_attn, qkv, q_rope, attn_out, attn_proj, ff, ff_down, logits,
+      argmax_max, argmax_idx, token, pos, workspace;
 };
 
 // Prefill activations: cap rows.
@@ -189,13 +189,20 @@ int record_decode_step(grout_engine* e) {
                          "embedding"));
   for (int l = 0; l < c.num_layers; ++l) {
     const grout_qwen3_layer& w = e->layers[l];
+    // input norm fused into the QKV GEMV (layer 0: plain RMSNorm of the
+    // embedding; later layers: add the previous layer's MLP output first)
     if (l == 0)
-      GROUT_CHECK(norm(e, nullptr, e->d(b.hidden), w.input_layernorm, e->d(b.normed), nullptr, 1));
+      GROUT_CHECK(hip_status(grout::launch_gemv_norm(w.qkv_proj, nullptr, e->d(b.hidden),
+                                                     w.input_layernorm, nullptr, c.rms_norm_eps,
+                                                     e->d(b.qkv), e->qkv_dim, c.hidden_size,
+                                                     false, s),
+                             "qkv gemv"));
     else
-      GROUT_CHECK(norm(e, e->d(b.hidden_after_attn), e->d(b.ff_down), w.input_layernorm,
-                       e->d(b.normed), e->d(b.hidden), 1));
-    GROUT_CHECK(project(e, w.qkv_proj, e->d(b.normed), e->d(b.qkv), 1, e->qkv_dim,
-                        c.hidden_size));
+      GROUT_CHECK(hip_status(grout::launch_gemv_norm(w.qkv_proj, e->d(b.hidden_after_attn),
+                                                     e->d(b.ff_down), w.input_layernorm,
+                                                     e->d(b.hidden), c.rms_norm_eps, e->d(b.qkv),
+                                                     e->qkv_dim, c.hidden_size, false, s),
+                             "qkv gemv"));
     GROUT_CHECK(grout_qk_norm_rope_kv_decode(
         e->d(b.qkv), w.q_norm, w.k_norm, e->rope_cos(), e->rope_sin(), e->d(b.q_rope),
         e->k_cache(l), e->v_cache(l), e->d<uint32_t>(b.pos), c.num_q_heads, c.num_kv_heads, 128,
@@ -206,13 +213,14 @@ int record_decode_step(grout_engine* e) {
                                   e->num_splits, e->qk_scale, s));
     GROUT_CHECK(project(e, w.o_proj, e->d(b.attn_out), e->d(b.attn_proj), 1, c.hidden_size,
                         e->q_dim));
-    GROUT_CHECK(norm(e, e->d(b.hidden), e->d(b.attn_proj), w.post_attention_layernorm,
-                     e->d(b.ff_normed), e->d(b.hidden_after_attn), 1));
-    GROUT_CHECK(project(e, w.gate_up_proj, e->d(b.ff_normed), e->d(b.gate_up), 1,
-                        2 * c.intermediate_size, c.hidden_size));
-    GROUT_CHECK(hip_status(grout::launch_silu_mul(e->d(b.gate_up), e->d(b.ff), 1,
-                                                  c.intermediate_size, s),
-                           "silu_mul"));
+    // post-attention add + RMSNorm fused into the gate_up GEMV, whose
+    // epilogue applies SiLU(gate) * up: it writes ff directly
+    GROUT_CHECK(hip_status(grout::launch_gemv_norm(w.gate_up_proj, e->d(b.hidden),
+                                                   e->d(b.attn_proj), w.post_attention_layernorm,
+                                                   e->d(b.hidden_after_attn), c.rms_norm_eps,
+                                                   e->d(b.ff), c.intermediate_size,
+                                                   c.hidden_size, true, s),
+                           "gate_up gemv"));
     GROUT_CHECK(project(e, w.down_proj, e->d(b.ff), e->d(b.ff_down), 1, c.hidden_size,
                         c.intermediate_size));
   }
@@ -396,8 +404,6 @@ int create_impl(grout_engine* e, const grout_qwen3_config* c, const grout_qwen3_
   b.q_rope = a.take(e->q_dim * h2);
   b.attn_out = a.take(e->q_dim * h2);
   b.attn_proj = a.take(H * h2);
-  b.ff_normed = a.take(H * h2);
-  b.gate_up = a.take(2 * I * h2);
   b.ff = a.take(I * h2);
   b.ff_down = a.take(H * h2);
   b.logits = a.take((size_t)c->vocab_size * h2);
@@ -480,6 +486,35 @@ int grout_gemv(const void* W, const void* x, void* y, int n, int k, void* stream
   GROUT_NEED(y != nullptr && (reinterpret_cast<uintptr_t>(y) & 1u) == 0, GROUT_EALIGN,
              "y is NULL or not 2-byte aligned");
   return hip_status(grout::launch_gemv(W, x, y, n, k, as_stream(stream)), "gemv launch");
+}
+
+static int check_gemv_norm(const void* W, const void* residual, const void* x,
+                           const void* gamma, void* residual_out, void* y, int n, int k,
+                           float eps) {
+  GROUT_NEED(n >= 1, GROUT_EINVAL, "n=%d", n);
+  GROUT_CHECK(check_norm(1, k, eps));
+  GROUT_CHECK(check_ptrs16({{W, "W"}, {x, "x"}, {gamma, "gamma"}}));
+  if (residual) GROUT_CHECK(check_ptrs16({{residual, "residual"}, {residual_out, "residual_out"}}));
+  GROUT_NEED(y != nullptr && (reinterpret_cast<uintptr_t>(y) & 1u) == 0, GROUT_EALIGN,
+             "y is NULL or not 2-byte aligned");
+  return GROUT_OK;
+}
+
+int grout_gemv_rms_norm(const void* W, const void* residual, const void* x, const void* gamma,
+                        void* residual_out, void* y, int n, int k, float eps, void* stream) {
+  GROUT_CHECK(check_gemv_norm(W, residual, x, gamma, residual_out, y, n, k, eps));
+  return hip_status(grout::launch_gemv_norm(W, residual, x, gamma, residual_out, eps, y, n, k,
+                                            false, as_stream(stream)),
+                    "gemv_rms_norm launch");
+}
+
+int grout_gemv_rms_norm_silu_mul(const void* W, const void* residual, const void* x,
+                                 const void* gamma, void* residual_out, void* y, int inter, int k,
+                                 float eps, void* stream) {
+  GROUT_CHECK(check_gemv_norm(W, residual, x, gamma, residual_out, y, inter, k, eps));
+  return hip_status(grout::launch_gemv_norm(W, residual, x, gamma, residual_out, eps, y, inter,
+                                            k, true, as_stream(stream)),
+                    "gemv_rms_norm_silu_mul launch");
 }
 
 size_t grout_argmax_workspace_bytes(int vocab_size) {

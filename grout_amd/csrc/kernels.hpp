@@ -42,6 +42,12 @@ hipError_t launch_rms_norm(const void* residual, const void* x, const void* w, v
                            void* residual_out, int rows, int H, float eps, hipStream_t stream);
 hipError_t launch_silu_mul(const void* gate_up, void* out, int rows, int I, hipStream_t stream);
 hipError_t launch_gemv(const void* W, const void* x, void* y, int N, int K, hipStream_t stream);
+// GEMV whose input is the RMSNorm (residual == nullptr) or add-RMSNorm of x,
+// computed per wave; the first wave writes residual_out = residual + x.
+// silu_pairs: W holds 2N rows [gate | up] and y[n] = silu(gate_n) * up_n.
+hipError_t launch_gemv_norm(const void* W, const void* residual, const void* x, const void* gamma,
+                            void* residual_out, float eps, void* y, int N, int K, bool silu_pairs,
+                            hipStream_t stream);
 int argmax_num_blocks(int V);
 hipError_t launch_argmax(const void* logits, float* block_max, uint32_t* block_idx, int V,
                          uint32_t* out, hipStream_t stream);

@@ -96,6 +96,27 @@ int grout_silu_mul(const void* gate_up, void* out, int rows, int inter, void* st
  * reference, src/cublas.rs:434-570). */
 int grout_gemv(const void* W, const void* x, void* y, int n, int k, void* stream);
 
+/* y = W . x' where x' = rms_norm(x) * gamma (residual == NULL) or
+ * x' = rms_norm(residual + x) * gamma, rounded to f16 as the separate norm
+ * kernels round it; with a residual, residual_out = f16(residual + x) is
+ * written too (it must not alias residual or x).  The decode step's input and
+ * post-attention norms fused into the QKV / gate_up GEMVs: one launch for
+ * rms_norm_f16 or add_rms_norm_decode_raw_f16 (src/kernels.rs:1530-1569,
+ * 4518-4657) followed by the projection GEMV (src/model.rs:3427-3474,
+ * 3819-3848).  k = hidden size, a multiple of 8 in [8, 8192]. */
+int grout_gemv_rms_norm(const void* W, const void* residual, const void* x, const void* gamma,
+                        void* residual_out, void* y, int n, int k, float eps, void* stream);
+
+/* As grout_gemv_rms_norm for W = gate_up_proj [2*inter][k] (rows [gate | up]),
+ * with SiLU * up applied in the epilogue: y[i] = f16(silu(g_i) * u_i) for
+ * i < inter, g_i and u_i the f16 products of gate row i and up row i.  The
+ * decode step's post-attention add-RMSNorm, gate_up GEMV and silu_mul_2d_f16
+ * (src/kernels.rs:4518-4657, 1493-1522; src/model.rs:3819-3880) in one
+ * launch. */
+int grout_gemv_rms_norm_silu_mul(const void* W, const void* residual, const void* x,
+                                 const void* gamma, void* residual_out, void* y, int inter, int k,
+                                 float eps, void* stream);
+
 /* Scratch bytes grout_argmax needs for vocab_size logits. */
 size_t grout_argmax_workspace_bytes(int vocab_size);
 

@@ -114,6 +114,86 @@ def test_gemv(gpu, n, k):
     assert np.all(err <= ulp(ref) + 1e-6 * mag + 1e-7)
 
 
+@pytest.mark.parametrize("mode", ["norm", "add_norm"])
+@pytest.mark.parametrize("n,k", [(6144, 2560), (19456, 2560), (100, 8192), (3, 64)])
+def test_gemv_rms_norm_fused(gpu, mode, n, k):
+    """Norm fused into the GEMV vs the oracle's norm then product.  The fused
+    input rounds like the separate kernel; its 1/rms may differ in the last
+    bit (another summation order), flipping single fp16 inputs by one ulp:
+    |err| <= 1 ulp + 1e-6 sum|w x| + 1e-4."""
+    L = gpu.lib()
+    print(f"gemv_rms_norm {mode} n={n} k={k}", flush=True)
+    W = Q.f16_bits(O.h2f(O.fill_normal_f16(O.seed_for(f"fw{n}"), (n, k))) * 0.02)
+    x = O.fill_normal_f16(O.seed_for(f"fx{k}"), (k,))
+    r = O.fill_normal_f16(O.seed_for(f"fr{k}"), (k,))
+    g = O.fill_uniform_f16(O.seed_for(f"fg{k}"), 0.8, 1.2, (k,))
+    dW, dx, dr, dg = dev(W), dev(x), dev(r), dev(g)
+    y = torch.empty(n, dtype=torch.float16, device="cuda")
+    res_out = torch.full((k,), 3.0, dtype=torch.float16, device="cuda")
+    if mode == "norm":
+        call(L, "grout_gemv_rms_norm", ptr(dW), None, ptr(dx), ptr(dg), None, ptr(y), n, k,
+             C.c_float(1e-6), None)
+        xn = Q.rms_norm(x[None], g, 1e-6)[0]
+    else:
+        call(L, "grout_gemv_rms_norm", ptr(dW), ptr(dr), ptr(dx), ptr(dg), ptr(res_out), ptr(y),
+             n, k, C.c_float(1e-6), None)
+        xn, ref_res = Q.add_rms_norm(r[None], x[None], g, 1e-6)
+        xn = xn[0]
+    torch.cuda.synchronize()
+    if mode == "add_norm":
+        assert np.array_equal(host(res_out), ref_res[0])
+    Wf, xf = O.h2f(W).astype(np.float64), O.h2f(xn).astype(np.float64)
+    ref = Wf @ xf
+    mag = np.abs(Wf) @ np.abs(xf)
+    err = np.abs(O.h2f(host(y)).astype(np.float64) - ref)
+    print(f"[gemv_rms_norm] max_err={err.max():.3e}", flush=True)
+    assert np.all(err <= ulp(ref) + 1e-6 * mag + 1e-4)
+
+
+@pytest.mark.parametrize("mode", ["norm", "add_norm"])
+@pytest.mark.parametrize("inter,k", [(9728, 2560), (64, 8), (5, 4104), (300, 5120)])
+def test_gemv_rms_norm_silu_mul_fused(gpu, mode, inter, k):
+    """gate_up GEMV with the norm input and SiLU * up epilogue vs the oracle's
+    norm -> product -> silu_mul.  Tolerance: the gate/up products may differ
+    from the oracle by the GEMV bound; the SiLU * up of those values is then
+    within that bound times |d(silu(g) u)| plus one ulp of the output."""
+    L = gpu.lib()
+    print(f"gemv_rms_norm_silu_mul {mode} inter={inter} k={k}", flush=True)
+    W = Q.f16_bits(O.h2f(O.fill_normal_f16(O.seed_for(f"gu{inter}"), (2 * inter, k))) * 0.05)
+    x = O.fill_normal_f16(O.seed_for(f"gx{k}"), (k,))
+    r = O.fill_normal_f16(O.seed_for(f"gr{k}"), (k,))
+    g = O.fill_uniform_f16(O.seed_for(f"gg{k}"), 0.8, 1.2, (k,))
+    dW, dx, dr, dg = dev(W), dev(x), dev(r), dev(g)
+    y = torch.empty(inter, dtype=torch.float16, device="cuda")
+    res_out = torch.empty(k, dtype=torch.float16, device="cuda")
+    if mode == "norm":
+        call(L, "grout_gemv_rms_norm_silu_mul", ptr(dW), None, ptr(dx), ptr(dg), None, ptr(y),
+             inter, k, C.c_float(1e-6), None)
+        xn = Q.rms_norm(x[None], g, 1e-6)[0]
+    else:
+        call(L, "grout_gemv_rms_norm_silu_mul", ptr(dW), ptr(dr), ptr(dx), ptr(dg), ptr(res_out),
+             ptr(y), inter, k, C.c_float(1e-6), None)
+        xn, ref_res = Q.add_rms_norm(r[None], x[None], g, 1e-6)
+        xn = xn[0]
+    torch.cuda.synchronize()
+    if mode == "add_norm":
+        assert np.array_equal(host(res_out), ref_res[0])
+    gu = Q.linear(xn[None], W)  # f16 gate|up as the unfused path stores them
+    ref = O.h2f(Q.silu_mul(gu, inter)[0]).astype(np.float64)
+    Wf, xf = O.h2f(W).astype(np.float64), O.h2f(xn).astype(np.float64)
+    mag = np.abs(Wf) @ np.abs(xf)
+    guf = O.h2f(gu[0]).astype(np.float64)
+    prod_tol = ulp(guf) + 1e-6 * mag + 1e-4  # bound on each gate/up product
+    gg, uu = guf[:inter], guf[inter:]
+    sig = 1 / (1 + np.exp(-gg))
+    dg = np.abs(uu * sig * (1 + gg * (1 - sig)))  # d/dg of silu(g) * u
+    du = np.abs(gg * sig)
+    tol = dg * prod_tol[:inter] + du * prod_tol[inter:] + 1.5 * ulp(ref) + 1e-7
+    err = np.abs(O.h2f(host(y)).astype(np.float64) - ref)
+    print(f"[gemv_rms_norm_silu_mul] max_err={err.max():.3e}", flush=True)
+    assert np.all(err <= tol)
+
+
 def test_embedding(gpu):
     L = gpu.lib()
     V, H = 1000, 2560
