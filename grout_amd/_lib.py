@@ -64,6 +64,8 @@ SIGNATURES = {
     "grout_attn_decode": (_i, [_p, _p, _p, _p, _p, _sz, _p, _i, _i, _i, _i, _l, _i, _f, _p]),
     "grout_fmha_decode_gqa_split": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _l, _i, _f, _p]),
     "grout_splitk_reduce_merge": (_i, [_p, _p, _p, _i, _i, _i, _i, _p]),
+    "grout_attn_decode_fused": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p, _i, _i, _i, _i,
+                                     _l, _i, _f, _f, _p]),
     "grout_decode_graph_create": (_i, [C.POINTER(DecodeLayer), _i, _p, _p, _p, _sz, _i, _i, _i,
                                        _i, _i, _f, _f, _p, C.POINTER(_p)]),
     "grout_decode_graph_launch": (_i, [_p, _u32, _p]),

@@ -202,6 +202,43 @@ int grout_attn_decode(const void* q, const void* k_cache, const void* v_cache, v
                     "attn_decode merge launch");
 }
 
+int grout_attn_decode_fused(const void* qkv, const void* gamma_q, const void* gamma_k,
+                            const float* rope_cos, const float* rope_sin, void* k_cache,
+                            void* v_cache, void* out, void* workspace, size_t workspace_bytes,
+                            const uint32_t* d_pos, int num_q_heads, int num_kv_heads,
+                            int head_dim, int max_ctx, long kv_head_stride, int num_splits,
+                            float eps, float qk_scale, void* stream) {
+  GROUT_CHECK(check_heads(num_q_heads, num_kv_heads, head_dim, kMaxDecodeGroup));
+  if (num_splits <= 0) num_splits = grout_attn_decode_default_splits(max_ctx, num_q_heads, num_kv_heads);
+  GROUT_NEED(num_splits <= kMaxSplits, GROUT_EINVAL, "num_splits=%d > %d", num_splits, kMaxSplits);
+  GROUT_NEED(max_ctx >= 1, GROUT_EINVAL, "max_ctx=%d", max_ctx);
+  GROUT_NEED(std::isfinite(eps) && eps > 0.f, GROUT_EINVAL, "eps=%g", (double)eps);
+  GROUT_NEED(std::isfinite(qk_scale) && qk_scale > 0.f, GROUT_EINVAL, "qk_scale=%g",
+             (double)qk_scale);
+  GROUT_NEED(d_pos != nullptr && rope_cos != nullptr && rope_sin != nullptr, GROUT_EINVAL,
+             "d_pos or a rope table is NULL");
+  GROUT_CHECK(check_ptrs16({{qkv, "qkv"}, {gamma_q, "gamma_q"}, {gamma_k, "gamma_k"},
+                            {k_cache, "k_cache"}, {v_cache, "v_cache"}, {out, "out"}}));
+  GROUT_CHECK(check_stride(kv_head_stride, max_ctx));
+  float* part_acc = nullptr;
+  float* part_ml = nullptr;
+  if (num_splits > 1) {
+    const size_t need = decode_ws_bytes(num_q_heads, num_kv_heads, num_splits);
+    GROUT_NEED(workspace != nullptr && workspace_bytes >= need, GROUT_EINVAL,
+               "workspace of %zu bytes < %zu needed for %d splits", workspace_bytes, need,
+               num_splits);
+    GROUT_CHECK(check_ptrs16({{workspace, "workspace"}}));
+    part_acc = static_cast<float*>(workspace);
+    part_ml = part_acc + (size_t)num_kv_heads * num_splits * (num_q_heads / num_kv_heads) * 128;
+  }
+  return hip_status(grout::launch_attn_decode_fused(qkv, gamma_q, gamma_k, rope_cos, rope_sin,
+                                                    k_cache, v_cache, kv_head_stride, d_pos,
+                                                    max_ctx, num_q_heads, num_kv_heads,
+                                                    num_splits, eps, qk_scale, part_acc, part_ml,
+                                                    out, as_stream(stream)),
+                    "attn_decode_fused launch");
+}
+
 // ------------------------------------------------------------------ graph
 
 struct grout_decode_graph {

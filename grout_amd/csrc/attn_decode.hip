@@ -36,11 +36,13 @@
 //    atomics, both of which serialize at ~0.3-1 us per split.)
 #include "common.hpp"
 #include "kernels.hpp"
+#include "qk_norm_rope.hpp"
 
 namespace grout {
 
 constexpr int kTile = 16;    // kv positions per wave step
-constexpr int kDecWaves = 4;
+constexpr int kDecWaves = 4;  // waves per workgroup of the split pass
+constexpr int kDirectWaves = 8;  // waves per workgroup of the one-split pass
 constexpr int kSlotBytes = 2 * kTile * kHeadDim * 2;  // 8 KiB per wave: K rows then V rows
 constexpr float kDecRescaleThreshold = 8.0f;
 
@@ -55,15 +57,39 @@ __device__ __forceinline__ floatx4 mfma16x16x16(half4 a, half4 b, floatx4 c) {
 // j ^ dswz(r); a bijection on r % 16 whose upper three bits are r % 8.
 __device__ __forceinline__ int dswz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
 
-__global__ __launch_bounds__(kDecWaves * 64, 2) void attn_decode_split_kernel(
+// Inputs of the fused variant: the raw QKV projection of the new token
+// instead of rotated q rows, and what the norm/RoPE/KV write needs.
+struct DecodeFused {
+  const half_t* qkv;      // [Q (Hq*128) | K (Hkv*128) | V (Hkv*128)]
+  const half_t* gamma_q;  // [128]
+  const half_t* gamma_k;  // [128]
+  const float* rope_cos;  // [max_ctx][64]
+  const float* rope_sin;
+  half_t* k_cache;        // writable views of the caches (row pos is written)
+  half_t* v_cache;
+  float eps;
+  int Hq;
+};
+
+// WAVES waves per workgroup (split, kv head).  FUSED: the workgroup first
+// computes its G rotated q rows (into LDS) and, if its split holds position
+// pos, the new K row and V row of its kv head: it writes them to the cache
+// and patches them into its own LDS copy of the last tile (rows pos .. end of
+// that tile, which the loads clamp to row pos), so no other kernel and no
+// memory ordering is involved.  DIRECT (one split): the normalized f16
+// output goes straight to out [Hq][128] instead of the fp32 partials.
+template <int WAVES, bool FUSED, bool DIRECT>
+__global__ __launch_bounds__(WAVES * 64, (WAVES <= 4 ? 2 : 1)) void attn_decode_split_kernel(
     const half_t* __restrict__ q, const half_t* __restrict__ k_cache,
     const half_t* __restrict__ v_cache, long head_stride, const uint32_t* __restrict__ d_pos,
     int max_ctx, int G, int nsplit, float scale_log2, float* __restrict__ part_acc,
-    float* __restrict__ part_ml) {
+    float* __restrict__ part_ml, DecodeFused fz, half_t* __restrict__ out) {
   // Wave w's tile buffer is s_buf[w]; after the loop the buffers are reused
   // for the cross-wave merge.
-  __shared__ __attribute__((aligned(1024))) unsigned char s_buf[kDecWaves][kSlotBytes];
-  __shared__ float s_ml[kDecWaves][16][2];
+  __shared__ __attribute__((aligned(1024))) unsigned char s_buf[WAVES][kSlotBytes];
+  __shared__ float s_ml[WAVES][16][2];
+  // FUSED: rotated q rows of the group, then the new K and V rows.
+  __shared__ __attribute__((aligned(16))) half_t s_qkv[FUSED ? 18 : 1][kHeadDim];
 
   const int split = blockIdx.x, kvh = blockIdx.y;
   const int lane = threadIdx.x & 63;
@@ -77,29 +103,68 @@ __global__ __launch_bounds__(kDecWaves * 64, 2) void attn_decode_split_kernel(
   const int per = (ntiles + nsplit - 1) / nsplit;
   const int t0 = split * per;
   const int t1 = min(t0 + per, ntiles);
-  // this wave's tiles: t0 + w + 4k, k = 0 .. nmine-1
-  const int nmine = t0 + w < t1 ? (t1 - t0 - w + kDecWaves - 1) / kDecWaves : 0;
+  // this wave's tiles: t0 + w + WAVES k, k = 0 .. nmine-1
+  const int nmine = t0 + w < t1 ? (t1 - t0 - w + WAVES - 1) / WAVES : 0;
 
-  // Wave w takes the split's tiles j = w + 4k, visited from j = rot on
-  // (cyclically; rot is a multiple of 4, so the tile sets stay disjoint).
+  // Wave w takes the split's tiles j = w + WAVES k, visited from j = rot on
+  // (cyclically; rot is a multiple of WAVES, so the tile sets stay disjoint).
   // Splits start 256 KiB apart at 32k; staggering where each one starts
   // spreads the concurrent reads over more HBM channels (measured a few
   // percent at 4k context, within noise at 32k).
   const int len = t1 - t0;
-  const int rot = len > 0 && len % 4 == 0 ? ((split * 7 + kvh * 3) % (len / 4)) * 4 : 0;
+  const int rot =
+      len > 0 && len % WAVES == 0 ? ((split * 7 + kvh * 3) % (len / WAVES)) * WAVES : 0;
   auto tile_of = [&](int k) __attribute__((always_inline)) {
-    const int x = w + kDecWaves * k + rot;
+    const int x = w + WAVES * k + rot;
     return t0 + (x >= len ? x - len : x);
   };
 
   const unsigned char* kh = reinterpret_cast<const unsigned char*>(k_cache + (size_t)kvh * head_stride);
   const unsigned char* vh = reinterpret_cast<const unsigned char*>(v_cache + (size_t)kvh * head_stride);
 
+  // FUSED prologue: 32-lane group gi of the workgroup normalizes and rotates
+  // rows gi, gi + 2 WAVES, ...: rows 0..G-1 are the group's q heads, row G
+  // (owner only) the new K row; the owner also stages the V row.
+  const int t_new = s_kv - 1 - (s_kv - 1) % kTile;  // first position of the last tile
+  const bool owner = FUSED && pos < (uint32_t)max_ctx && t_new / kTile >= t0 &&
+                     t_new / kTile < t1;
+  if constexpr (FUSED) {
+    const int gi = threadIdx.x >> 5, j = threadIdx.x & 31;
+    const int nrows = G + (owner ? 1 : 0);
+    // a position past the cache writes nothing; its q rows use the last
+    // table row so every read stays in bounds
+    const uint32_t rpos = pos < (uint32_t)max_ctx ? pos : (uint32_t)max_ctx - 1;
+    const size_t trow = (size_t)rpos * (kHeadDim / 2) + 4 * (j & 15);
+    for (int r = gi; r < nrows; r += 2 * WAVES) {  // uniform per 32-lane group
+      const bool is_k = r == G;
+      const half_t* x = fz.qkv + (size_t)(is_k ? fz.Hq + kvh : kvh * G + r) * kHeadDim;
+      const u32x2 xr = *reinterpret_cast<const u32x2*>(x + 4 * j);
+      const half4 gh = __builtin_bit_cast(
+          half4, *reinterpret_cast<const u32x2*>((is_k ? fz.gamma_k : fz.gamma_q) + 4 * j));
+      const floatx4 c = *reinterpret_cast<const floatx4*>(fz.rope_cos + trow);
+      const floatx4 sn = *reinterpret_cast<const floatx4*>(fz.rope_sin + trow);
+      const u32x2 yr = norm_rope_row(xr, gh, c, sn, j, fz.eps);
+      *reinterpret_cast<u32x2*>(&s_qkv[r][4 * j]) = yr;
+      if (is_k) {
+        const u32x2 vr = *reinterpret_cast<const u32x2*>(
+            fz.qkv + (size_t)(fz.Hq + (int)gridDim.y + kvh) * kHeadDim + 4 * j);
+        *reinterpret_cast<u32x2*>(&s_qkv[G + 1][4 * j]) = vr;
+        const size_t coff = (size_t)kvh * head_stride + (size_t)pos * kHeadDim + 4 * j;
+        *reinterpret_cast<u32x2*>(fz.k_cache + coff) = yr;
+        *reinterpret_cast<u32x2*>(fz.v_cache + coff) = vr;
+      }
+    }
+    __syncthreads();
+  }
+
   half8 qf[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     if (col < G) {
-      qf[c] = as_half8(load16(q + ((size_t)kvh * G + col) * kHeadDim + c * 32 + kb * 8));
+      if constexpr (FUSED)
+        qf[c] = as_half8(*reinterpret_cast<const u32x4*>(&s_qkv[col][c * 32 + kb * 8]));
+      else
+        qf[c] = as_half8(load16(q + ((size_t)kvh * G + col) * kHeadDim + c * 32 + kb * 8));
     } else {
       qf[c] = as_half8(u32x4{0u, 0u, 0u, 0u});
     }
@@ -203,6 +268,18 @@ __global__ __launch_bounds__(kDecWaves * 64, 2) void attn_decode_split_kernel(
     }
     if (k + 1 < nmine) load_tile(k + 1);
     store_tile(ck, cv);  // after this wave's reads of the previous tile (LDS is in order)
+    if (FUSED && owner && tile_of(k) * kTile == t_new) {
+      // rows pos .. t_new+15 of the slot get the new K / V row (the loads
+      // read the cache's old row pos for all of them)
+      const int r0 = (int)pos - t_new;
+      const int chunk = lane & 15, kv = (lane >> 4) & 1;  // lanes 0..31: 16 K + 16 V chunks
+      if (lane < 32) {
+        const u32x4 v16 = *reinterpret_cast<const u32x4*>(&s_qkv[G + kv][chunk * 8]);
+        for (int r = r0; r < kTile; ++r)
+          *reinterpret_cast<u32x4*>(&s_buf[0][0] + wave_off + kv * 4096 + r * 256 +
+                                    ((chunk ^ dswz(r)) << 4)) = v16;
+      }
+    }
     compute(k, &s_buf[0][0]);
   }
   __syncthreads();  // all waves are done with their tile buffers before they are reused
@@ -222,22 +299,26 @@ __global__ __launch_bounds__(kDecWaves * 64, 2) void attn_decode_split_kernel(
   __syncthreads();
 
   const size_t base = ((size_t)kvh * nsplit + split) * G;
-  for (int e = threadIdx.x; e < G * kHeadDim; e += kDecWaves * 64) {
+  for (int e = threadIdx.x; e < G * kHeadDim; e += WAVES * 64) {
     const int g = e / kHeadDim, d = e - g * kHeadDim;
     float M = s_ml[0][g][0];
 #pragma unroll
-    for (int ww = 1; ww < kDecWaves; ++ww) M = fmaxf(M, s_ml[ww][g][0]);
+    for (int ww = 1; ww < WAVES; ++ww) M = fmaxf(M, s_ml[ww][g][0]);
     float L = 0.f, O = 0.f;
 #pragma unroll
-    for (int ww = 0; ww < kDecWaves; ++ww) {
+    for (int ww = 0; ww < WAVES; ++ww) {
       const float wgt = fast_exp2(s_ml[ww][g][0] - M);
       L += wgt * s_ml[ww][g][1];
       O += wgt * s_acc[ww][g][d];
     }
-    part_acc[(base + g) * kHeadDim + d] = O;
-    if (d == 0) {
-      part_ml[(base + g) * 2 + 0] = M;
-      part_ml[(base + g) * 2 + 1] = L;
+    if constexpr (DIRECT) {
+      out[((size_t)kvh * G + g) * kHeadDim + d] = (half_t)(O / L);
+    } else {
+      part_acc[(base + g) * kHeadDim + d] = O;
+      if (d == 0) {
+        part_ml[(base + g) * 2 + 0] = M;
+        part_ml[(base + g) * 2 + 1] = L;
+      }
     }
   }
 }
@@ -302,10 +383,36 @@ hipError_t launch_attn_decode_split(const void* q, const void* k_cache, const vo
                                     float* part_acc, float* part_ml, hipStream_t stream) {
   const float scale_log2 = qk_scale * 1.4426950408889634f;
   dim3 grid((unsigned)nsplit, (unsigned)Hkv);
-  attn_decode_split_kernel<<<grid, kDecWaves * 64, 0, stream>>>(
+  attn_decode_split_kernel<kDecWaves, false, false><<<grid, kDecWaves * 64, 0, stream>>>(
       (const half_t*)q, (const half_t*)k_cache, (const half_t*)v_cache, head_stride, d_pos,
-      max_ctx, Hq / Hkv, nsplit, scale_log2, part_acc, part_ml);
+      max_ctx, Hq / Hkv, nsplit, scale_log2, part_acc, part_ml, DecodeFused{}, nullptr);
   return hipGetLastError();
+}
+
+hipError_t launch_attn_decode_fused(const void* qkv, const void* gamma_q, const void* gamma_k,
+                                    const float* rope_cos, const float* rope_sin, void* k_cache,
+                                    void* v_cache, long head_stride, const uint32_t* d_pos,
+                                    int max_ctx, int Hq, int Hkv, int nsplit, float eps,
+                                    float qk_scale, float* part_acc, float* part_ml, void* out,
+                                    hipStream_t stream) {
+  const float scale_log2 = qk_scale * 1.4426950408889634f;
+  const DecodeFused fz{(const half_t*)qkv, (const half_t*)gamma_q, (const half_t*)gamma_k,
+                       rope_cos, rope_sin, (half_t*)k_cache, (half_t*)v_cache, eps, Hq};
+  if (Hq / Hkv > 16) return hipErrorInvalidValue;
+  if (nsplit == 1) {
+    attn_decode_split_kernel<kDirectWaves, true, true>
+        <<<dim3(1u, (unsigned)Hkv), kDirectWaves * 64, 0, stream>>>(
+            nullptr, (const half_t*)k_cache, (const half_t*)v_cache, head_stride, d_pos, max_ctx,
+            Hq / Hkv, 1, scale_log2, nullptr, nullptr, fz, (half_t*)out);
+    return hipGetLastError();
+  }
+  attn_decode_split_kernel<kDecWaves, true, false>
+      <<<dim3((unsigned)nsplit, (unsigned)Hkv), kDecWaves * 64, 0, stream>>>(
+          nullptr, (const half_t*)k_cache, (const half_t*)v_cache, head_stride, d_pos, max_ctx,
+          Hq / Hkv, nsplit, scale_log2, part_acc, part_ml, fz, nullptr);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return launch_attn_decode_merge(part_acc, part_ml, out, Hq, Hkv, nsplit, stream);
 }
 
 hipError_t launch_attn_decode_merge(const float* part_acc, const float* part_ml, void* out,

@@ -55,7 +55,7 @@ struct Arena {
 
 // Decode-step activations: one token.
 struct DecodeBufs {
-  size_t hidden, normed, hidden_after_attn, qkv, q_rope, attn_out, attn_proj, ff, ff_down, logits,
+  size_t hidden, normed, hidden_after_attn, qkv, attn_out, attn_proj, ff, ff_down, logits,
       argmax_max, argmax_idx, token, pos, workspace;
 };
 
@@ -203,14 +203,12 @@ int record_decode_step(grout_engine* e) {
                                                      e->d(b.hidden), c.rms_norm_eps, e->d(b.qkv),
                                                      e->qkv_dim, c.hidden_size, false, s),
                              "qkv gemv"));
-    GROUT_CHECK(grout_qk_norm_rope_kv_decode(
-        e->d(b.qkv), w.q_norm, w.k_norm, e->rope_cos(), e->rope_sin(), e->d(b.q_rope),
-        e->k_cache(l), e->v_cache(l), e->d<uint32_t>(b.pos), c.num_q_heads, c.num_kv_heads, 128,
-        c.max_ctx, e->head_stride, c.rms_norm_eps, s));
-    GROUT_CHECK(grout_attn_decode(e->d(b.q_rope), e->k_cache(l), e->v_cache(l), e->d(b.attn_out),
-                                  e->d(b.workspace), e->ws_bytes, e->d<uint32_t>(b.pos),
-                                  c.num_q_heads, c.num_kv_heads, 128, c.max_ctx, e->head_stride,
-                                  e->num_splits, e->qk_scale, s));
+    // QK-norm/RoPE + K/V cache write inside the split-K attention, then the merge
+    GROUT_CHECK(grout_attn_decode_fused(
+        e->d(b.qkv), w.q_norm, w.k_norm, e->rope_cos(), e->rope_sin(), e->k_cache(l),
+        e->v_cache(l), e->d(b.attn_out), e->d(b.workspace), e->ws_bytes,
+        e->d<uint32_t>(b.pos), c.num_q_heads, c.num_kv_heads, 128, c.max_ctx, e->head_stride,
+        e->num_splits, c.rms_norm_eps, e->qk_scale, s));
     GROUT_CHECK(project(e, w.o_proj, e->d(b.attn_out), e->d(b.attn_proj), 1, c.hidden_size,
                         e->q_dim));
     // post-attention add + RMSNorm fused into the gate_up GEMV, whose
@@ -401,7 +399,6 @@ int create_impl(grout_engine* e, const grout_qwen3_config* c, const grout_qwen3_
   b.normed = a.take(H * h2);
   b.hidden_after_attn = a.take(H * h2);
   b.qkv = a.take(e->qkv_dim * h2);
-  b.q_rope = a.take(e->q_dim * h2);
   b.attn_out = a.take(e->q_dim * h2);
   b.attn_proj = a.take(H * h2);
   b.ff = a.take(I * h2);

@@ -27,6 +27,15 @@ hipError_t launch_attn_decode_split(const void* q, const void* k_cache, const vo
                                     int Hq, int Hkv, int nsplit, float qk_scale,
                                     float* part_acc, float* part_ml, hipStream_t stream);
 
+// Fused decode step of one layer: QK-RMSNorm + RoPE of the new token's q
+// rows and K row, K/V cache write at d_pos[0], and split-K attention; one
+// split (nsplit == 1) writes out directly, more splits add the merge launch.
+hipError_t launch_attn_decode_fused(const void* qkv, const void* gamma_q, const void* gamma_k,
+                                    const float* rope_cos, const float* rope_sin, void* k_cache,
+                                    void* v_cache, long head_stride, const uint32_t* d_pos,
+                                    int max_ctx, int Hq, int Hkv, int nsplit, float eps,
+                                    float qk_scale, float* part_acc, float* part_ml, void* out,
+                                    hipStream_t stream);
 hipError_t launch_attn_decode_merge(const float* part_acc, const float* part_ml, void* out,
                                     int Hq, int Hkv, int nsplit, hipStream_t stream);
 

@@ -21,39 +21,11 @@
 // an IEEE-defined operation that a CPU performs identically.
 #include "common.hpp"
 #include "kernels.hpp"
+#include "qk_norm_rope.hpp"
 
 #pragma clang fp contract(off)
 
 namespace grout {
-
-__device__ __forceinline__ float rsqrt_det(float v) {
-  uint32_t b = __builtin_bit_cast(uint32_t, v);
-  b = 0x5f3759dfu - (b >> 1);
-  double y = (double)__builtin_bit_cast(float, b);
-  const double vd = (double)v;
-#pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    double t = vd * y;
-    t = t * y;
-    t = 0.5 * t;
-    t = 1.5 - t;
-    y = y * t;
-  }
-  return (float)y;
-}
-
-// Lane exchanges inside one 32-lane row group, on the VALU (no LDS round
-// trip): xor16 swaps the two 16-lane halves, ror(N) reads lane (l+N) mod 16 of
-// the same half.
-__device__ __forceinline__ float xor16(float x) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  // r[0]: odd halves take the even half's value; r[1]: even halves take the odd half's
-  return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
-}
-template <int N>
-__device__ __forceinline__ float ror16(float x) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x120 + N, 0xf, 0xf, false));
-}
 
 // Grid (tokens, ceil((Hq+Hkv)/(8R))): 32-lane group g of the 256-thread
 // workgroup takes heads h = 8R*blockIdx.y + g + 8r (r < R) of token
@@ -115,51 +87,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv_kernel(
     if (h >= H) continue;  // uniform across the group
     const bool is_q = h < Hq;
     const int kvh = h - Hq;
-    const half4 xh = __builtin_bit_cast(half4, xr[r]);
-    const float x0 = (float)xh[0], x1 = (float)xh[1], x2 = (float)xh[2], x3 = (float)xh[3];
-
-    // Sum of squares: fixed tree, in-lane (a^2+b^2)+(c^2+d^2) then the
-    // butterfly over partners l^16, l^8, l^4, l^2, l^1.  After the l^16 and
-    // l^8 steps lanes l and l^8 hold equal values, so the rotation partners
-    // (l+-4, l+-2, l+-1 mod 16) add exactly the values the xor partners would.
-    float a0 = x0 * x0, a1 = x1 * x1, a2 = x2 * x2, a3 = x3 * x3;
-    float s0 = a0 + a1, s1 = a2 + a3;
-    float ss = s0 + s1;
-    ss = ss + xor16(ss);
-    ss = ss + ror16<8>(ss);
-    ss = ss + ror16<4>(ss);
-    ss = ss + ror16<2>(ss);
-    ss = ss + ror16<1>(ss);
-    const float mean = ss / (float)kHeadDim;
-    const float inv = rsqrt_det(mean + eps);
-
-    const half4 gh = is_q ? gq : gk;
-    float n[4];
-    n[0] = (x0 * inv) * (float)gh[0];
-    n[1] = (x1 * inv) * (float)gh[1];
-    n[2] = (x2 * inv) * (float)gh[2];
-    n[3] = (x3 * inv) * (float)gh[3];
-    float p[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) p[i] = xor16(n[i]);  // RoPE partner (d +/- 64)
-
-    half4 y;
-    if (j < 16) {  // low half: y = n_lo*c - n_hi*s
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float t0 = n[i] * c[i];
-        float t1 = p[i] * sn[i];
-        y[i] = (half_t)(t0 - t1);
-      }
-    } else {  // high half: y = n_hi*c + n_lo*s
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float t0 = n[i] * c[i];
-        float t1 = p[i] * sn[i];
-        y[i] = (half_t)(t0 + t1);
-      }
-    }
-    const u32x2 yr = __builtin_bit_cast(u32x2, y);
+    const u32x2 yr = norm_rope_row(xr[r], is_q ? gq : gk, c, sn, j, eps);
     if (is_q) {
       half_t* dst = kDecode ? q_out + (size_t)h * kHeadDim : q_out + ((size_t)s * Hq + h) * kHeadDim;
       *reinterpret_cast<u32x2*>(dst + 4 * j) = yr;

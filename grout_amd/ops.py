@@ -140,6 +140,32 @@ def attn_decode(q, k_cache, v_cache, position: torch.Tensor, num_splits: Optiona
     return out.view(q.shape)
 
 
+def attn_decode_fused(qkv, q_norm, k_norm, rope, k_cache, v_cache, position: torch.Tensor,
+                      num_q_heads: int, num_splits: Optional[int] = None, out=None,
+                      workspace=None, eps: float = 1e-6,
+                      qk_scale: Optional[float] = None) -> torch.Tensor:
+    """One layer's decode attention from the raw QKV projection: QK-RMSNorm +
+    RoPE + K/V cache write at `position`, then split-K attention (one launch
+    for num_splits == 1).  qkv [(Hq+2Hkv)*D]; returns out [Hq, D]."""
+    Hkv, max_ctx, D = k_cache.shape
+    Hq = num_q_heads
+    _f16(qkv, "qkv", ((Hq + 2 * Hkv) * D,))
+    _f16(k_cache, "k_cache")
+    _f16(v_cache, "v_cache", tuple(k_cache.shape))
+    cos, sin = rope
+    _need(cos.shape[0] >= max_ctx, "rope tables shorter than the cache")
+    ns = default_splits(max_ctx, Hq, Hkv) if not num_splits else num_splits
+    if workspace is None and ns > 1:
+        workspace = decode_workspace(Hq, Hkv, ns, qkv.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    out = torch.empty((Hq, D), dtype=torch.float16, device=qkv.device) if out is None else out
+    qk_scale = 1.0 / math.sqrt(D) if qk_scale is None else qk_scale
+    call("grout_attn_decode_fused", _ptr(qkv), _ptr(q_norm), _ptr(k_norm), _ptr(cos), _ptr(sin),
+         _ptr(k_cache), _ptr(v_cache), _ptr(out), _ptr(workspace), ws_bytes, _ptr(position), Hq,
+         Hkv, D, max_ctx, max_ctx * D, ns, eps, qk_scale, _stream(qkv.device))
+    return out
+
+
 def fmha_decode_gqa_split(q, k_cache, v_cache, position, num_splits: int,
                           qk_scale: Optional[float] = None):
     """The split pass alone: returns (part_acc [Hkv, splits, G, D], part_ml [Hkv, splits, G, 2])."""

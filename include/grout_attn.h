@@ -142,6 +142,27 @@ int grout_splitk_reduce_merge(const float* part_acc, const float* part_ml, void*
                               int num_q_heads, int num_kv_heads, int head_dim, int num_splits,
                               void* stream);
 
+/* One layer's attention of a decode step in one launch (two with more than
+ * one split): the QK-RMSNorm + RoPE of the new token's q heads and K head and
+ * the K/V cache write at d_pos[0] (grout_qk_norm_rope_kv_decode), then the
+ * split-K attention over positions 0 .. d_pos[0] (grout_attn_decode), with
+ * the rotated q rows kept on chip.  qkv, gammas, rope tables and caches as in
+ * grout_qk_norm_rope_kv_decode; out [Hq][128].  num_splits == 1 writes out
+ * directly (no workspace needed, workspace may be NULL); num_splits > 1 uses
+ * grout_attn_decode_workspace_bytes(..., num_splits) of workspace and adds
+ * the merge launch; num_splits <= 0 picks the default for max_ctx.  A
+ * position >= max_ctx writes nothing.  K/V cache rows are bit-identical to
+ * grout_qk_norm_rope_kv_decode's.
+ * Replaces the decode graph's qk_norm_rope_kv_decode_raw_f16 +
+ * fmha_decode_gqa_split + splitk_reduce_merge records (src/model.rs:3492-3519,
+ * 3713-3771; src/kernels.rs:3996-4304, 5170-5452). */
+int grout_attn_decode_fused(const void* qkv, const void* gamma_q, const void* gamma_k,
+                            const float* rope_cos, const float* rope_sin, void* k_cache,
+                            void* v_cache, void* out, void* workspace, size_t workspace_bytes,
+                            const uint32_t* d_pos, int num_q_heads, int num_kv_heads,
+                            int head_dim, int max_ctx, long kv_head_stride, int num_splits,
+                            float eps, float qk_scale, void* stream);
+
 /* ------------------------------------------------------------------ */
 /* Decode-step graph (a8)                                              */
 /* ------------------------------------------------------------------ */

@@ -118,6 +118,44 @@ def test_decode_attention_vs_oracle(gpu, Hq, Hkv, ctx, max_ctx, splits):
     _decode_case(gpu, Hq, Hkv, ctx, max_ctx, splits, f"dec{Hq}_{ctx}")
 
 
+@pytest.mark.parametrize("Hq,Hkv,pos,max_ctx,splits", [
+    (32, 8, 640, 1024, 1),        # engine shape, one split (direct output)
+    (32, 8, 640, 1024, None),     # default splits + merge
+    (32, 8, 4095, 4096, 1),
+    (64, 8, 8191, 32768, None),   # 32B, G = 8
+    (32, 2, 100, 160, 3),         # G = 16, ragged
+    (40, 8, 16, 64, 1),           # G = 5, the new row opens a tile
+    (8, 8, 0, 64, 1),             # first position
+    (16, 8, 47, 64, 7),           # more splits than tiles
+])
+def test_fused_decode_step_vs_oracle(gpu, Hq, Hkv, pos, max_ctx, splits):
+    """Norm/RoPE/KV write fused into the decode attention: cache rows
+    bit-exact against the oracle's norm/RoPE/KV write, output within the
+    attention tolerance of the oracle's attention on the oracle's q rows.
+    Cache rows past pos hold NaN: the tile loads clamp to row pos, which the
+    kernel patches with the new row, so they never reach the output."""
+    _say("fused_decode", Hq, Hkv, pos, max_ctx, splits)
+    qkv = normal("fqkv", ((Hq + 2 * Hkv) * D,))
+    gq, gk = gamma("fgq"), gamma("fgk")
+    cos, sin = O.rope_table(max_ctx, D, 1e6)
+    kc = normal("fkc", (Hkv, max_ctx, D))
+    vc = normal("fvc", (Hkv, max_ctx, D))
+    kc[:, pos:, :] = 0x7E00  # NaN: the cache's old row pos and everything after it
+    vc[:, pos:, :] = 0x7E00
+    kc_ref, vc_ref = kc.copy(), vc.copy()
+    q_ref = O.qk_norm_rope_kv_decode(qkv, gq, gk, cos, sin, kc_ref, vc_ref, pos, Hq, Hkv, 1e-6)
+    ref = O.attention_decode(q_ref, kc_ref, vc_ref, pos, nthreads=8)
+    rope = gpu.ops.rope_tables(max_ctx)
+    kc_d, vc_d = dev(kc), dev(vc)
+    p = torch.tensor([pos], dtype=torch.int32, device="cuda")
+    out = gpu.ops.attn_decode_fused(dev(qkv), dev(gq), dev(gk), rope, kc_d, vc_d, p, Hq,
+                                    num_splits=splits)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(kc_d), kc_ref)
+    assert np.array_equal(host(vc_d), vc_ref)
+    assert_close(host_f32(out), ref, f"fused decode Hq={Hq} pos={pos} splits={splits}")
+
+
 def test_decode_split_then_merge_matches_fused_call(gpu):
     Hq, Hkv, ctx, max_ctx, ns = 32, 8, 3000, 4096, 11
     q, kc, vc = normal("sq", (Hq, D)), normal("sk", (Hkv, max_ctx, D)), normal("sv", (Hkv, max_ctx, D))
