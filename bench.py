@@ -189,6 +189,35 @@ def bench_norm(ops, S, Hq, Hkv, max_ctx, steps, warmup):
     return dict(ms=ms, alg_bytes=alg_bytes)
 
 
+def bench_fused_attention(Hq, Hkv, ctx, max_ctx, n_layers, steps, warmup):
+    """Per-layer decode attention as the engine's decode graph runs it
+    (grout_attn_decode_fused: norm/RoPE/KV write + split-K, then the merge),
+    over n_layers rotating caches; ms per layer."""
+    import torch
+    from grout_amd import ops
+
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(11)
+    kcs = [torch.randn((Hkv, max_ctx, D), generator=g, device=dev, dtype=torch.float16)
+           for _ in range(n_layers)]
+    vcs = [torch.randn((Hkv, max_ctx, D), generator=g, device=dev, dtype=torch.float16)
+           for _ in range(n_layers)]
+    qkv = torch.randn(((Hq + 2 * Hkv) * D,), generator=g, device=dev, dtype=torch.float16)
+    gam = torch.ones(D, dtype=torch.float16, device=dev)
+    rope = ops.rope_tables(max_ctx, device=dev)
+    pos = torch.tensor([ctx - 1], dtype=torch.int32, device=dev)
+    out = torch.empty((Hq, D), dtype=torch.float16, device=dev)
+    ns = ops.default_splits(max_ctx, Hq, Hkv)
+    ws = ops.decode_workspace(Hq, Hkv, ns, dev)
+    ms = time_launches(lambda i: ops.attn_decode_fused(qkv, gam, gam, rope, kcs[i % n_layers],
+                                                       vcs[i % n_layers], pos, Hq, num_splits=ns,
+                                                       out=out, workspace=ws),
+                       steps, warmup)
+    del kcs, vcs
+    torch.cuda.empty_cache()
+    return ms
+
+
 def bench_engine(prompt_len=512, decode_steps=256, max_ctx=1024):
     """Config 5: Qwen3-4B-shaped engine, random N(0, 0.02) fp16 weights (norm
     weights 1), a seeded uniform prompt prefilled, then greedy decode steps,
@@ -347,10 +376,9 @@ def main():
     if want("engine4b"):
         res["engine4b"] = bench_engine()
         # attention part of one decode step at the mean context of the run:
-        # the 36-layer graph of norm/RoPE/KV write + split + merge
-        res["engine4b"]["attn_graph_ms"] = bench_decode_graph(
-            grout_amd, 32, 8, int(res["engine4b"]["mean_ctx"]), 1024, 36,
-            max(a.steps // 4, 10), a.warmup)
+        # 36 layers of the fused norm/RoPE/KV write + split-K + merge
+        res["engine4b"]["attn_graph_ms"] = 36 * bench_fused_attention(
+            32, 8, int(res["engine4b"]["mean_ctx"]), 1024, 36, a.steps, a.warmup)
         print(f"# engine4b {res['engine4b']}", file=sys.stderr, flush=True)
 
     line = {"metric": "decode-attn HBM GB/s (% of peak) + prefill FMHA TFLOP/s (% MFMA peak)",
