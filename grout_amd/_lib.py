@@ -85,6 +85,7 @@ SIGNATURES = {
     "grout_engine_create": (_i, [C.POINTER(Qwen3Config), C.POINTER(Qwen3Weights), _i,
                                  C.POINTER(_p)]),
     "grout_engine_prefill": (_i, [_p, _p, _i, _p, _p]),
+    "grout_engine_extend": (_i, [_p, _p, _i, _p, _p]),
     "grout_engine_decode": (_i, [_p, _u32, _p]),
     "grout_engine_decode_greedy": (_i, [_p, _u32, _p]),
     "grout_engine_reset": (_i, [_p]),

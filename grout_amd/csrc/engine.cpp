@@ -555,13 +555,19 @@ int grout_engine_create(const grout_qwen3_config* config, const grout_qwen3_weig
   return GROUT_OK;
 }
 
-int grout_engine_prefill(grout_engine* e, const uint32_t* tokens, int n, float* logits_out,
-                         uint32_t* next_token) {
-  GROUT_NEED(e != nullptr, GROUT_EINVAL, "engine is NULL");
-  GROUT_CHECK(take_pending(e));
+}  // extern "C"
+
+namespace {
+
+// Runs tokens[0..n) at positions pos0 .. pos0+n-1 through every layer (their
+// K/V rows land in the caches; rows < pos0 must already hold the session's
+// earlier tokens), then the head over the last one.
+int run_chunk(grout_engine* e, const uint32_t* tokens, int n, int pos0, float* logits_out,
+              uint32_t* next_token) {
   const auto& c = e->cfg;
   GROUT_NEED(tokens != nullptr && n >= 1, GROUT_EINVAL, "prefill requires at least one token");
-  GROUT_NEED(n <= c.max_ctx, GROUT_EINVAL, "prefill length %d exceeds max_ctx=%d", n, c.max_ctx);
+  GROUT_NEED((long)pos0 + n <= c.max_ctx, GROUT_EINVAL,
+             "prefill of %d tokens at position %d exceeds max_ctx=%d", n, pos0, c.max_ctx);
   for (int i = 0; i < n; ++i)
     GROUT_NEED(tokens[i] < (uint32_t)c.vocab_size, GROUT_EINVAL,
                "token %u at %d >= vocab_size=%d", tokens[i], i, c.vocab_size);
@@ -592,10 +598,10 @@ int grout_engine_prefill(grout_engine* e, const uint32_t* tokens, int n, float* 
                         n, e->kv_dim, H));
     GROUT_CHECK(grout_qk_norm_rope_kv_prefill(
         e->p(b.q), e->p(b.k), e->p(b.v), w.q_norm, w.k_norm, e->rope_cos(), e->rope_sin(),
-        e->p(b.q_rope), e->k_cache(l), e->v_cache(l), 0, n, c.num_q_heads, c.num_kv_heads, 128,
-        c.max_ctx, e->head_stride, c.rms_norm_eps, s));
+        e->p(b.q_rope), e->k_cache(l), e->v_cache(l), pos0, n, c.num_q_heads, c.num_kv_heads,
+        128, c.max_ctx, e->head_stride, c.rms_norm_eps, s));
     GROUT_CHECK(grout_fmha_prefill(e->p(b.q_rope), e->k_cache(l), e->v_cache(l),
-                                   e->p(b.attn_out), n, 0, c.num_q_heads, c.num_kv_heads, 128,
+                                   e->p(b.attn_out), n, pos0, c.num_q_heads, c.num_kv_heads, 128,
                                    e->head_stride, e->qk_scale, s));
     GROUT_CHECK(project(e, w.o_proj, e->p(b.attn_out), e->p(b.attn_proj), n, H, e->q_dim));
     GROUT_CHECK(norm(e, e->p(b.hidden), e->p(b.attn_proj), w.post_attention_layernorm,
@@ -609,9 +615,28 @@ int grout_engine_prefill(grout_engine* e, const uint32_t* tokens, int n, float* 
   const size_t last = (size_t)(n - 1) * H;
   GROUT_CHECK(head(e, e->p<uint16_t>(b.hidden_after_attn) + last, e->p<uint16_t>(b.ff_down) + last));
   GROUT_CHECK(copy_logits_out(e, logits_out, next_token));
-  e->next_pos = n;
+  e->next_pos = pos0 + n;
   e->session_active = true;
   return GROUT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int grout_engine_prefill(grout_engine* e, const uint32_t* tokens, int n, float* logits_out,
+                         uint32_t* next_token) {
+  GROUT_NEED(e != nullptr, GROUT_EINVAL, "engine is NULL");
+  GROUT_CHECK(take_pending(e));
+  return run_chunk(e, tokens, n, 0, logits_out, next_token);
+}
+
+int grout_engine_extend(grout_engine* e, const uint32_t* tokens, int n, float* logits_out,
+                        uint32_t* next_token) {
+  GROUT_NEED(e != nullptr, GROUT_EINVAL, "engine is NULL");
+  GROUT_CHECK(take_pending(e));
+  GROUT_NEED(e->session_active, GROUT_EINVAL, "extend requires a preceding prefill");
+  return run_chunk(e, tokens, n, e->next_pos, logits_out, next_token);
 }
 
 int grout_engine_decode(grout_engine* e, uint32_t token, float* logits_out) {

@@ -203,6 +203,17 @@ class Engine:
              C.byref(tok))
         return int(tok.value)
 
+    def extend(self, tokens: Sequence[int]) -> Logits:
+        """Chunked prefill: runs `tokens` at the session's next positions
+        (grout_engine_extend) and returns the last one's logits."""
+        ids = np.ascontiguousarray(np.asarray(tokens, dtype=np.int64), dtype=np.uint32)
+        if ids.ndim != 1 or ids.size == 0:
+            raise ValueError("extend requires at least one token")
+        out = np.empty(self.cfg.vocab_size, np.float32)
+        call("grout_engine_extend", self._h, ids.ctypes.data_as(C.c_void_p), ids.size,
+             out.ctypes.data_as(C.c_void_p), None)
+        return Logits(out)
+
     # -- src/api.rs:110-121
     def decode(self, token: int) -> Logits:
         out = np.empty(self.cfg.vocab_size, np.float32)

@@ -148,6 +148,18 @@ int grout_engine_create(const grout_qwen3_config* config, const grout_qwen3_weig
 int grout_engine_prefill(grout_engine* engine, const uint32_t* tokens, int n_tokens,
                          float* logits_out, uint32_t* next_token);
 
+/* Chunked prefill: runs tokens[0..n_tokens) at the session's next positions
+ * (after a prefill, extends, or decodes), with the same prefill kernels at
+ * pos0 = grout_engine_position(); outputs as grout_engine_prefill.  Requires
+ * an active session and position + n_tokens <= max_ctx.  An invalid argument
+ * leaves the session as it was; a failure while running ends it (the next
+ * call must be a prefill).  The reference's kernels take
+ * a prefill start position but its API only issues new sessions
+ * (src/model.rs:2126); this is that path, e.g. for prompts longer than one
+ * chunk or multi-turn input. */
+int grout_engine_extend(grout_engine* engine, const uint32_t* tokens, int n_tokens,
+                        float* logits_out, uint32_t* next_token);
+
 /* Decodes `token` at the next position of the session (one replay of the
  * decode-step graph) and writes next-token logits (f32, vocab_size floats).
  * Requires a preceding prefill and position < max_ctx.

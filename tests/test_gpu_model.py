@@ -305,6 +305,64 @@ def test_engine_prefill_and_decode_vs_oracle(gpu, name, n_prompt, n_decode, max_
         eng.close()
 
 
+@pytest.mark.parametrize("name,chunks", [("g2", [20, 1, 13]), ("g8", [64, 100, 7])])
+def test_engine_chunked_prefill_vs_oracle(gpu, name, chunks):
+    """Chunked prefill (grout_engine_extend, prefill kernels at pos0 > 0): each
+    chunk's last logits against the oracle run over the same chunks, then a
+    decode step; a one-shot prefill of all chunks agrees with the chunked
+    session within the same tolerance."""
+    cfg = tiny_configs()[name]
+    print(f"engine chunked {name} chunks={chunks}", flush=True)
+    host_w = Q.random_host_weights(cfg, seed=31, std=0.05)
+    toks = np.random.default_rng(sum(chunks)).integers(0, cfg.vocab_size, sum(chunks))
+    parts = np.split(toks, np.cumsum(chunks)[:-1])
+    eng = make_engine(cfg, host_w, 256)
+    orc = Q.Qwen3Oracle(cfg, host_w, 256)
+    try:
+        got = eng.prefill(parts[0]).values
+        ref, _ = orc.forward(parts[0], 0, nthreads=8)
+        check_logits(got, ref, f"{name} chunk 0")
+        pos = len(parts[0])
+        for i, part in enumerate(parts[1:], 1):
+            got = eng.extend(part).values
+            ref, _ = orc.forward(part, pos, nthreads=8)
+            pos += len(part)
+            check_logits(got, ref, f"{name} chunk {i}")
+            assert eng.position == pos
+        tok = int(np.argmax(got))
+        got = eng.decode(tok).values
+        ref, _ = orc.forward([tok], pos, nthreads=8)
+        check_logits(got, ref, f"{name} decode after chunks")
+        eng.reset()
+        whole = eng.prefill(toks).values
+        ref_whole, _ = Q.Qwen3Oracle(cfg, host_w, 256).forward(toks, 0, nthreads=8)
+        check_logits(whole, ref_whole, f"{name} one-shot prefill")
+    finally:
+        eng.close()
+
+
+def test_engine_extend_errors(gpu):
+    from grout_amd._lib import GroutError
+
+    cfg = tiny_configs()["g2"]
+    eng = make_engine(cfg, Q.random_host_weights(cfg, seed=2), 16)
+    try:
+        with pytest.raises(GroutError, match="preceding prefill"):
+            eng.extend([1, 2])
+        eng.prefill(list(range(10)))
+        with pytest.raises(GroutError, match="exceeds max_ctx"):
+            eng.extend(list(range(7)))
+        with pytest.raises(GroutError, match="vocab_size"):
+            eng.extend([cfg.vocab_size])
+        assert eng.position == 10  # rejected arguments leave the session as it was
+        eng.extend(list(range(6)))
+        assert eng.position == 16
+        with pytest.raises(GroutError, match="exceeds max_ctx"):
+            eng.decode_greedy(1)
+    finally:
+        eng.close()
+
+
 def test_engine_greedy_matches_logits_and_reset_is_clean(gpu):
     cfg = tiny_configs()["g2"]
     host_w = Q.random_host_weights(cfg, seed=4, std=0.05)
