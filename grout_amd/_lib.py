@@ -48,6 +48,11 @@ class Qwen3Weights(C.Structure):
                 ("layers", C.POINTER(Qwen3Layer))]
 
 
+class ModelInfo(C.Structure):
+    _fields_ = [("config", Qwen3Config), ("tie_word_embeddings", _i), ("num_eos", _i),
+                ("eos_token_ids", _u32 * 8), ("weight_bytes", _sz)]
+
+
 # name -> (restype, argtypes).  Every symbol declared in include/*.h.
 SIGNATURES = {
     "grout_last_error": (C.c_char_p, []),
@@ -84,6 +89,13 @@ SIGNATURES = {
     "grout_argmax": (_i, [_p, _i, _p, _sz, _p, _p]),
     "grout_engine_create": (_i, [C.POINTER(Qwen3Config), C.POINTER(Qwen3Weights), _i,
                                  C.POINTER(_p)]),
+    "grout_model_inspect": (_i, [C.c_char_p, C.POINTER(ModelInfo)]),
+    "grout_model_load": (_i, [C.c_char_p, _i, C.POINTER(_p)]),
+    "grout_model_get_info": (_i, [_p, C.POINTER(ModelInfo)]),
+    "grout_model_weights": (_i, [_p, C.POINTER(Qwen3Weights)]),
+    "grout_model_free": (_i, [_p]),
+    "grout_engine_load": (_i, [C.c_char_p, _i, _i, C.POINTER(_p)]),
+    "grout_engine_model_info": (_i, [_p, C.POINTER(ModelInfo)]),
     "grout_engine_prefill": (_i, [_p, _p, _i, _p, _p]),
     "grout_engine_extend": (_i, [_p, _p, _i, _p, _p]),
     "grout_engine_decode": (_i, [_p, _u32, _p]),

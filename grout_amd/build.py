@@ -32,6 +32,7 @@ SOURCES = [
     ("model_kernels.hip", []),
     ("api.cpp", ["-x", "hip"]),
     ("engine.cpp", ["-x", "hip"]),
+    ("loader.cpp", ["-x", "hip"]),
 ]
 # Prefill projections are plain GEMMs: rocBLAS.
 LIBS = ["-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"]

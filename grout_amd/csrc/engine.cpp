@@ -116,6 +116,9 @@ struct grout_engine {
   bool session_active = false;
   std::string pending_reset_error;
 
+  // Set by grout_engine_load: the checkpoint's weights, freed with the engine.
+  grout_model* owned_model = nullptr;
+
   void* k_cache(int l) const {
     return static_cast<char*>(kv) + (size_t)l * 2 * cache_bytes();
   }
@@ -684,7 +687,42 @@ int grout_engine_destroy(grout_engine* e) {
   if (e->h_logits) (void)hipHostFree(e->h_logits);
   if (e->h_token) (void)hipHostFree(e->h_token);
   if (e->stream) (void)hipStreamDestroy(e->stream);
+  grout_model* m = e->owned_model;
   delete e;
+  return grout_model_free(m);
+}
+
+int grout_engine_load(const char* model_dir, int max_ctx, int device, grout_engine** out) {
+  GROUT_NEED(out != nullptr, GROUT_EINVAL, "out is NULL");
+  *out = nullptr;
+  GROUT_NEED(max_ctx >= 0, GROUT_EINVAL, "max_ctx=%d", max_ctx);
+  grout_model* m = nullptr;
+  GROUT_CHECK(grout_model_load(model_dir, device, &m));
+  grout_model_info info;
+  grout_qwen3_weights w;
+  (void)grout_model_get_info(m, &info);
+  (void)grout_model_weights(m, &w);
+  grout_qwen3_config cfg = info.config;
+  if (max_ctx > 0) cfg.max_ctx = max_ctx;
+  grout_engine* e = nullptr;
+  const int rc = grout_engine_create(&cfg, &w, device, &e);
+  if (rc != GROUT_OK) {
+    const std::string msg = g_last_error;
+    grout_model_free(m);
+    g_last_error = msg;
+    return rc;
+  }
+  e->owned_model = m;
+  *out = e;
+  return GROUT_OK;
+}
+
+int grout_engine_model_info(const grout_engine* e, grout_model_info* info) {
+  GROUT_NEED(e != nullptr && info != nullptr, GROUT_EINVAL, "engine or info is NULL");
+  GROUT_NEED(e->owned_model != nullptr, GROUT_EINVAL,
+             "engine was created from caller weights, not loaded from a model directory");
+  GROUT_CHECK(grout_model_get_info(e->owned_model, info));
+  info->config.max_ctx = e->cfg.max_ctx;
   return GROUT_OK;
 }
 

@@ -58,6 +58,10 @@ hipError_t launch_gemv_norm(const void* W, const void* residual, const void* x, 
                             void* residual_out, float eps, void* y, int N, int K, bool silu_pairs,
                             hipStream_t stream);
 int argmax_num_blocks(int V);
+// dst[i] = f16(src[i]) for n elements of dtype 0 = f16, 1 = bf16, 2 = f32,
+// 3 = f64 (through f32), round to nearest even.
+hipError_t launch_convert_to_f16(const void* src, int dtype, size_t n, void* dst,
+                                 hipStream_t stream);
 hipError_t launch_argmax(const void* logits, float* block_max, uint32_t* block_idx, int V,
                          uint32_t* out, hipStream_t stream);
 

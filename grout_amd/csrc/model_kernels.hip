@@ -448,6 +448,32 @@ __global__ __launch_bounds__(256) void argmax_reduce_kernel(const float* __restr
   }
 }
 
+// ------------------------------------------------------------- weight cast
+
+// Checkpoint tensors to f16 the way the reference's loader casts them
+// (src/loader.rs:702-740): bf16 -> f32 (exact) -> f16, f32 -> f16,
+// f64 -> f32 -> f16, each step round to nearest even (v_cvt_f16_f32 in the
+// default rounding mode; overflow becomes inf).
+__global__ __launch_bounds__(256) void convert_to_f16_kernel(const void* __restrict__ src,
+                                                            int dtype, size_t n,
+                                                            half_t* __restrict__ dst) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x) {
+    float f;
+    if (dtype == 1) {
+      f = __uint_as_float((uint32_t)static_cast<const uint16_t*>(src)[i] << 16);
+    } else if (dtype == 2) {
+      f = static_cast<const float*>(src)[i];
+    } else if (dtype == 3) {
+      f = (float)static_cast<const double*>(src)[i];
+    } else {
+      dst[i] = static_cast<const half_t*>(src)[i];
+      continue;
+    }
+    dst[i] = (half_t)f;
+  }
+}
+
 // ------------------------------------------------------------- launchers
 
 hipError_t launch_embedding(const uint32_t* ids, const void* table, void* out, int rows, int H,
@@ -557,6 +583,15 @@ hipError_t launch_gemv_norm(const void* W, const void* residual, const void* x, 
 }
 
 int argmax_num_blocks(int V) { return (V + kArgmaxBlock - 1) / kArgmaxBlock; }
+
+hipError_t launch_convert_to_f16(const void* src, int dtype, size_t n, void* dst,
+                                 hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  const size_t blocks = (n + 255) / 256;
+  convert_to_f16_kernel<<<(unsigned)(blocks < 16384 ? blocks : 16384), 256, 0, stream>>>(
+      src, dtype, n, (half_t*)dst);
+  return hipGetLastError();
+}
 
 hipError_t launch_argmax(const void* logits, float* block_max, uint32_t* block_idx, int V,
                          uint32_t* out, hipStream_t stream) {

@@ -21,6 +21,7 @@ from typing import Dict, List, Optional, Sequence
 import numpy as np
 import torch
 
+from ._lib import ModelInfo as _CModelInfo
 from ._lib import Qwen3Config as _CConfig
 from ._lib import Qwen3Layer as _CLayer
 from ._lib import Qwen3Weights as _CWeights
@@ -144,6 +145,25 @@ class Qwen3Weights:
                 need(L[k], shp, f"layer {i} {k}")
 
 
+def _config_from_info(info) -> "tuple[Qwen3Config, int]":
+    c = info.config
+    eos = tuple(int(info.eos_token_ids[i]) for i in range(info.num_eos))
+    cfg = Qwen3Config(c.num_layers, c.hidden_size, c.intermediate_size, c.num_q_heads,
+                      c.num_kv_heads, c.vocab_size, c.head_dim, float(c.rms_norm_eps),
+                      float(c.rope_theta), bool(info.tie_word_embeddings), eos)
+    return cfg, int(c.max_ctx)
+
+
+def inspect(model_dir: str) -> Dict:
+    """Host-only check of a Qwen3 safetensors directory (grout_model_inspect):
+    returns the config, max_position_embeddings and the fp16 weight bytes."""
+    info = _CModelInfo()
+    call("grout_model_inspect", str(model_dir).encode(), C.byref(info))
+    cfg, max_pos = _config_from_info(info)
+    return {"config": cfg, "max_position_embeddings": max_pos,
+            "weight_bytes": int(info.weight_bytes)}
+
+
 @dataclass
 class Logits:
     """Last-token logits copied to the host as f32 (src/api.rs:39-44)."""
@@ -182,6 +202,24 @@ class Engine:
         self._h = C.c_void_p()
         call("grout_engine_create", C.byref(c), C.byref(w), device_ord, C.byref(self._h))
         self._logits = np.empty(cfg.vocab_size, np.float32)
+
+    # -- src/api.rs:60-90
+    @classmethod
+    def load(cls, model_dir: str, max_ctx: int = 0, device_ord: int = 0) -> "Engine":
+        """Loads a Qwen3 safetensors directory (config.json, shards) onto the
+        GPU and builds the engine over it (grout_engine_load); max_ctx 0 =
+        max_position_embeddings."""
+        if max_ctx < 0:
+            raise ValueError("max_ctx must be >= 0")
+        self = cls.__new__(cls)
+        self._h = C.c_void_p()
+        call("grout_engine_load", str(model_dir).encode(), max_ctx, device_ord, C.byref(self._h))
+        info = _CModelInfo()
+        call("grout_engine_model_info", self._h, C.byref(info))
+        self.cfg, ctx = _config_from_info(info)
+        self.weights = None  # owned by the engine
+        self._meta = ModelMeta(self.cfg.vocab_size, tuple(self.cfg.eos_token_ids), "qwen3", ctx)
+        return self
 
     # -- src/api.rs:92-108
     def prefill(self, tokens: Sequence[int]) -> Logits:

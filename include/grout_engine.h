@@ -132,6 +132,44 @@ int grout_argmax(const void* logits, int vocab_size, void* workspace, size_t wor
 
 typedef struct grout_engine grout_engine;
 
+/* ------------------------------------------------------------------ */
+/* Checkpoint loading                                                  */
+/* ------------------------------------------------------------------ */
+
+#define GROUT_MAX_EOS 8
+
+/* What a model directory holds (config.json, generation_config.json). */
+typedef struct grout_model_info {
+  grout_qwen3_config config;  /* max_ctx = max_position_embeddings */
+  int tie_word_embeddings;
+  int num_eos;                /* stop tokens (generation_config.json, else config.json) */
+  uint32_t eos_token_ids[GROUT_MAX_EOS];
+  size_t weight_bytes;        /* device bytes of the fp16 weights in the fused layouts */
+} grout_model_info;
+
+typedef struct grout_model grout_model;
+
+/* Host only (no GPU): parses config.json, generation_config.json and the
+ * safetensors headers (model.safetensors.index.json + its shards, or a single
+ * model.safetensors) and checks that every tensor the engine needs is present
+ * with the expected shape and a castable dtype (F16/BF16/F32/F64).  Mirrors
+ * Loader::new + Qwen3Config::from_model_dir/validate (src/loader.rs:33-88,
+ * src/config.rs:24-95). */
+int grout_model_inspect(const char* model_dir, grout_model_info* info);
+
+/* grout_model_inspect, then the weights into one device allocation on
+ * `device` in the fused layouts (qkv_proj = q|k|v rows, gate_up_proj =
+ * gate|up rows, lm_head shared with embed_tokens when tied), bf16/f32/f64
+ * cast to f16 through f32 with round-to-nearest-even on the GPU.  Replaces
+ * the weight half of Qwen3Engine::load (src/model.rs:1508-1600) and
+ * cast_to_f16 (src/loader.rs:702-740). */
+int grout_model_load(const char* model_dir, int device, grout_model** out);
+int grout_model_get_info(const grout_model* model, grout_model_info* info);
+/* Device pointers of the loaded weights (valid until grout_model_free; the
+ * layers array belongs to the model). */
+int grout_model_weights(const grout_model* model, grout_qwen3_weights* weights);
+int grout_model_free(grout_model* model);
+
 /* Validates the configuration and every weight pointer, allocates the
  * engine's device state on `device` and captures the decode-step graph.
  * Mirrors Engine::load (src/api.rs:60-90) minus the file loading, with the
@@ -139,6 +177,15 @@ typedef struct grout_engine grout_engine;
  * 2631-4006). */
 int grout_engine_create(const grout_qwen3_config* config, const grout_qwen3_weights* weights,
                         int device, grout_engine** out);
+
+/* Engine::load (src/api.rs:60-90): grout_model_load + grout_engine_create
+ * with max_ctx (0 = max_position_embeddings); the engine owns the model and
+ * frees it in grout_engine_destroy. */
+int grout_engine_load(const char* model_dir, int max_ctx, int device, grout_engine** out);
+
+/* Info of the model an engine was loaded from (GROUT_EINVAL for engines made
+ * by grout_engine_create). */
+int grout_engine_model_info(const grout_engine* engine, grout_model_info* info);
 
 /* New-session prefill over tokens[0..n_tokens) (positions 0..n-1).  Writes
  * the last token's logits as f32 to logits_out (vocab_size floats, host

@@ -438,3 +438,81 @@ def test_engine_qwen3_4b_shapes_consistency(gpu):
         eng.close()
         del w
         torch.cuda.empty_cache()
+
+
+# ---------------------------------------------------------------- checkpoint loading
+
+
+def _d2h(ptr_value, shape):
+    """Copies fp16 device memory at a raw address to host bits (hipMemcpy)."""
+    hip = C.CDLL("libamdhip64.so")
+    out = np.empty(shape, np.uint16)
+    rc = hip.hipMemcpy(out.ctypes.data_as(C.c_void_p), C.c_void_p(ptr_value),
+                       C.c_size_t(out.nbytes), 2)  # device to host
+    assert rc == 0, rc
+    return out
+
+
+@pytest.mark.parametrize("tied,shards,dtypes", [
+    (True, 2, ("BF16", "F32", "F16", "F64")), (False, 1, ("F32", "BF16"))])
+def test_model_load_casts_and_fuses_bit_exact(gpu, tmp_path, tied, shards, dtypes):
+    """grout_model_load: every weight lands in the fused layout, cast to f16
+    through f32 with round-to-nearest-even (the reference's cast_to_f16)."""
+    from ckpt_util import write_checkpoint
+    from grout_amd._lib import ModelInfo, Qwen3Weights as CW
+    from grout_amd.model import Qwen3Config
+
+    cfg = Qwen3Config(num_layers=2, hidden_size=256, intermediate_size=512,
+                      num_attention_heads=4, num_key_value_heads=2, vocab_size=300,
+                      tie_word_embeddings=tied)
+    print(f"model_load tied={tied} shards={shards} dtypes={dtypes}", flush=True)
+    want = write_checkpoint(tmp_path, cfg, seed=5, dtypes=dtypes, shards=shards)
+    L = gpu.lib()
+    h = C.c_void_p()
+    call(L, "grout_model_load", str(tmp_path).encode(), 0, C.byref(h))
+    try:
+        w = CW()
+        call(L, "grout_model_weights", h, C.byref(w))
+        assert np.array_equal(_d2h(w.embed_tokens, want["embed_tokens"].shape), want["embed_tokens"])
+        assert np.array_equal(_d2h(w.norm, want["norm"].shape), want["norm"])
+        head = want["embed_tokens"] if tied else want["lm_head"]
+        assert np.array_equal(_d2h(w.lm_head, head.shape), head)
+        assert (w.lm_head == w.embed_tokens) == tied
+        for l in range(cfg.num_layers):
+            for k, arr in want["layers"][l].items():
+                got = _d2h(getattr(w.layers[l], k), arr.shape)
+                assert np.array_equal(got, arr), (l, k)
+        info = ModelInfo()
+        call(L, "grout_model_get_info", h, C.byref(info))
+        assert info.config.vocab_size == 300 and bool(info.tie_word_embeddings) == tied
+    finally:
+        L.grout_model_free(h)
+
+
+def test_engine_load_matches_oracle(gpu, tmp_path):
+    """Engine::load over a bf16 checkpoint directory: prefill + decode logits
+    against the oracle run on the same (cast) weights."""
+    from ckpt_util import write_checkpoint
+    from grout_amd.model import Engine, Qwen3Config
+
+    cfg = Qwen3Config(num_layers=2, hidden_size=512, intermediate_size=1024,
+                      num_attention_heads=8, num_key_value_heads=2, vocab_size=1000)
+    host_w = write_checkpoint(tmp_path, cfg, seed=9, dtypes=("BF16",), shards=2, max_pos=128,
+                              generation_eos=[7, 8])
+    eng = Engine.load(tmp_path)
+    orc = Q.Qwen3Oracle(cfg, host_w, 128)
+    try:
+        assert eng.meta().max_ctx == 128 and eng.meta().eos_token_ids == (7, 8)
+        prompt = list(np.random.default_rng(3).integers(0, 1000, 40))
+        got = eng.prefill(prompt).values
+        ref, _ = orc.prefill(prompt, nthreads=8)
+        tol = check_logits(got, ref, "loaded prefill")
+        tok = int(np.argmax(got))
+        check_token(tok, ref, tol, "loaded prefill token")
+        for i in range(3):
+            got = eng.decode(tok).values
+            ref, _ = orc.decode(tok, nthreads=8)
+            check_logits(got, ref, f"loaded decode {i}")
+            tok = int(np.argmax(got))
+    finally:
+        eng.close()
