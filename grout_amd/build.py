@@ -30,6 +30,7 @@ SOURCES = [
     ("attn_decode.hip", []),
     ("attn_prefill.hip", []),
     ("model_kernels.hip", []),
+    ("quant_gemv.hip", []),
     ("api.cpp", ["-x", "hip"]),
     ("engine.cpp", ["-x", "hip"]),
     ("loader.cpp", ["-x", "hip"]),

@@ -517,6 +517,52 @@ int grout_gemv_rms_norm_silu_mul(const void* W, const void* residual, const void
                     "gemv_rms_norm_silu_mul launch");
 }
 
+size_t grout_qweight_bytes(int fmt, int n, int k) { return grout::qweight_bytes(fmt, n, k); }
+
+static int check_q(int fmt, int n, int k) {
+  GROUT_NEED(fmt == GROUT_WFMT_Q8_0 || fmt == GROUT_WFMT_Q4_K || fmt == GROUT_WFMT_Q6_K,
+             GROUT_ENOTSUP, "weight format %d: Q8_0 (8), Q4_K (12) or Q6_K (14) expected", fmt);
+  GROUT_NEED(grout::qweight_bytes(fmt, n, k) != 0, GROUT_EINVAL,
+             "[%d][%d] of format %d: k must be a multiple of the block size and <= 16384", n, k,
+             fmt);
+  return GROUT_OK;
+}
+
+int grout_qweight_repack(int fmt, const void* ggml_blocks, int n, int k, void* out,
+                         void* stream) {
+  GROUT_CHECK(check_q(fmt, n, k));
+  GROUT_NEED(ggml_blocks != nullptr, GROUT_EINVAL, "ggml_blocks is NULL");
+  GROUT_CHECK(check_ptrs16({{out, "out"}}));
+  return hip_status(grout::launch_qweight_repack(fmt, ggml_blocks, n, k, out, as_stream(stream)),
+                    "qweight_repack launch");
+}
+
+int grout_gemv_q(int fmt, const void* wq, const void* x, void* y, int n, int k, void* stream) {
+  GROUT_CHECK(check_q(fmt, n, k));
+  GROUT_CHECK(check_ptrs16({{wq, "wq"}, {x, "x"}}));
+  GROUT_NEED(y != nullptr && (reinterpret_cast<uintptr_t>(y) & 1u) == 0, GROUT_EALIGN,
+             "y is NULL or not 2-byte aligned");
+  return hip_status(grout::launch_gemv_q(fmt, wq, x, y, n, k, false, as_stream(stream)),
+                    "gemv_q launch");
+}
+
+int grout_gemv_q_silu_mul(int fmt, const void* wq, const void* x, void* y, int inter, int k,
+                          void* stream) {
+  GROUT_CHECK(check_q(fmt, 2 * inter, k));
+  GROUT_CHECK(check_ptrs16({{wq, "wq"}, {x, "x"}}));
+  GROUT_NEED(y != nullptr && (reinterpret_cast<uintptr_t>(y) & 1u) == 0, GROUT_EALIGN,
+             "y is NULL or not 2-byte aligned");
+  return hip_status(grout::launch_gemv_q(fmt, wq, x, y, inter, k, true, as_stream(stream)),
+                    "gemv_q_silu_mul launch");
+}
+
+int grout_qweight_dequant(int fmt, const void* wq, int n, int k, void* out, void* stream) {
+  GROUT_CHECK(check_q(fmt, n, k));
+  GROUT_CHECK(check_ptrs16({{wq, "wq"}, {out, "out"}}));
+  return hip_status(grout::launch_qweight_dequant(fmt, wq, n, k, out, as_stream(stream)),
+                    "qweight_dequant launch");
+}
+
 size_t grout_argmax_workspace_bytes(int vocab_size) {
   if (vocab_size < 1) return 0;
   return (size_t)grout::argmax_num_blocks(vocab_size) * (sizeof(float) + sizeof(uint32_t));

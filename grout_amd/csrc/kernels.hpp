@@ -65,6 +65,17 @@ hipError_t launch_convert_to_f16(const void* src, int dtype, size_t n, void* dst
 hipError_t launch_argmax(const void* logits, float* block_max, uint32_t* block_idx, int V,
                          uint32_t* out, hipStream_t stream);
 
+// Low-bit decode GEMVs (quant_gemv.hip); fmt is the ggml type id: 8 = Q8_0,
+// 12 = Q4_K, 14 = Q6_K.  Weights in the repacked layout (qweight_bytes).
+size_t qweight_bytes(int fmt, int N, int K);
+hipError_t launch_qweight_repack(int fmt, const void* ggml_blocks, int N, int K, void* dst,
+                                 hipStream_t stream);
+// silu: W holds 2N rows [gate | up] and y[n] = silu(gate_n) * up_n.
+hipError_t launch_gemv_q(int fmt, const void* W, const void* x, void* y, int N, int K, bool silu,
+                         hipStream_t stream);
+hipError_t launch_qweight_dequant(int fmt, const void* W, int N, int K, void* out,
+                                  hipStream_t stream);
+
 // Writes the 16x16 C fragment of A x B for A[i][k] = i*32+k (k < 32), B = I
 // padded, one float per (lane, element): used to confirm the MFMA lane layout.
 hipError_t launch_mfma_layout_probe(float* out64x4, hipStream_t stream);

@@ -117,6 +117,40 @@ int grout_gemv_rms_norm_silu_mul(const void* W, const void* residual, const void
                                  const void* gamma, void* residual_out, void* y, int inter, int k,
                                  float eps, void* stream);
 
+/* ------------------------------------------------------------------ */
+/* Low-bit weights (ggml block formats, as GGUF files store them)      */
+/* ------------------------------------------------------------------ */
+
+#define GROUT_WFMT_F16 0    /* plain fp16 [n][k] */
+#define GROUT_WFMT_Q8_0 8   /* ggml type ids */
+#define GROUT_WFMT_Q4_K 12
+#define GROUT_WFMT_Q6_K 14
+
+/* Device bytes of an [n][k] matrix of format fmt in the GEMV layout (0 when
+ * the format or shape is unsupported: k a multiple of the block size, 32 for
+ * Q8_0 and 256 for the K-quants, at most 16384). */
+size_t grout_qweight_bytes(int fmt, int n, int k);
+
+/* Splits n rows of ggml blocks (device memory, rows contiguous) into the GEMV
+ * layout `out` (grout_qweight_bytes bytes); bytes are moved, not changed. */
+int grout_qweight_repack(int fmt, const void* ggml_blocks, int n, int k, void* out,
+                         void* stream);
+
+/* y[r] = f16(sum_k dequant(W)[r][k] x[k]), fp32 dequantization and
+ * accumulation.  Replaces gemv_q8_0_f16 / gemv_q4k_f16 / gemv_q6k_f16 and
+ * their SoA forms (src/kernels.rs:259-428, 564-804). */
+int grout_gemv_q(int fmt, const void* wq, const void* x, void* y, int n, int k, void* stream);
+
+/* wq holds 2*inter rows [gate | up]: y[i] = f16(silu(g_i) * u_i) with g_i,
+ * u_i the f16 products (the gate_up GEMV with silu_mul_2d_f16 in its
+ * epilogue, src/kernels.rs:1493-1522). */
+int grout_gemv_q_silu_mul(int fmt, const void* wq, const void* x, void* y, int inter, int k,
+                          void* stream);
+
+/* The [n][k] matrix dequantized to f16 (out), e.g. for prefill GEMMs
+ * (the reference's prefill dequant scratch, src/loader.rs:162). */
+int grout_qweight_dequant(int fmt, const void* wq, int n, int k, void* out, void* stream);
+
 /* Scratch bytes grout_argmax needs for vocab_size logits. */
 size_t grout_argmax_workspace_bytes(int vocab_size);
 

@@ -1,0 +1,120 @@
+/*
+ * ggml_quant.c -- CPU restatement of the quantized weight formats the
+ * reference's low-bit decode reads (TEST INFRASTRUCTURE ONLY: the checker for
+ * the HIP quantized GEMVs, never linked by the product).
+ *
+ * Formats (ggml block layouts, little endian), as dequantized by the
+ * reference's dequantize_q8_0 / dequantize_q4k / dequantize_q6k
+ * (src/dequant.rs:211-323) and get_scale_min_k4 (src/dequant.rs:325-335):
+ *
+ *   Q8_0  34 B per 32 weights:  f16 d; int8 q[32];            w = d*q
+ *   Q4_K 144 B per 256 weights: f16 d, dmin; u8 scales[12]; u8 qs[128]
+ *         sub-block s (32 weights) has 6-bit (sc, m) from scales;
+ *         group g (64 weights) = bytes qs[32g .. 32g+31]: low nibble of byte l
+ *         is weight 64g+l (sub-block 2g), high nibble weight 64g+32+l
+ *         (sub-block 2g+1);                                    w = d*sc*q - dmin*m
+ *   Q6_K 210 B per 256 weights: u8 ql[128]; u8 qh[64]; int8 sc[16]; f16 d
+ *         half n (128 weights), l < 32: 6-bit q = ql nibble | 2 bits of qh,
+ *         weights 128n + l + 32i (i = 0..3) use
+ *         i=0: ql[64n+l] low,    qh[32n+l] bits 0-1, sc[8n + l/16]
+ *         i=1: ql[64n+l+32] low, qh bits 2-3,        sc[8n + l/16 + 2]
+ *         i=2: ql[64n+l] high,   qh bits 4-5,        sc[8n + l/16 + 4]
+ *         i=3: ql[64n+l+32] high,qh bits 6-7,        sc[8n + l/16 + 6]
+ *                                                          w = d*sc*(q - 32)
+ * Every product is fp32 in the order the reference writes it.  The GEMV
+ * reference is y[n] = sum_k w[n][k] * x[k] accumulated in fp64 here (the
+ * reference accumulates in fp32, src/kernels.rs:259-428), so the GPU result
+ * differs from this only by fp32 rounding.
+ */
+#include <stddef.h>
+#include <stdint.h>
+#include <string.h>
+
+float go_h2f(uint16_t h);
+
+enum { GQ_Q8_0 = 8, GQ_Q4_K = 12, GQ_Q6_K = 14 };
+
+static uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* src/dequant.rs:325-335 */
+static void scale_min_k4(int j, const uint8_t* q, int* sc, int* m) {
+  if (j < 4) {
+    *sc = q[j] & 63;
+    *m = q[j + 4] & 63;
+  } else {
+    *sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+    *m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+  }
+}
+
+int go_qblock_bytes(int fmt) {
+  return fmt == GQ_Q8_0 ? 34 : fmt == GQ_Q4_K ? 144 : fmt == GQ_Q6_K ? 210 : -1;
+}
+int go_qblock_elems(int fmt) { return fmt == GQ_Q8_0 ? 32 : 256; }
+
+/* Dequantizes n weights (a multiple of the block size) into fp32. */
+int go_dequant(int fmt, const uint8_t* blocks, size_t n, float* out) {
+  const int be = go_qblock_elems(fmt), bb = go_qblock_bytes(fmt);
+  if (bb < 0 || n % (size_t)be) return -1;
+  for (size_t b = 0; b < n / (size_t)be; ++b) {
+    const uint8_t* x = blocks + b * (size_t)bb;
+    float* y = out + b * (size_t)be;
+    if (fmt == GQ_Q8_0) { /* src/dequant.rs:211-221 */
+      const float d = go_h2f(rd16(x));
+      for (int j = 0; j < 32; ++j) y[j] = (float)(int8_t)x[2 + j] * d;
+    } else if (fmt == GQ_Q4_K) { /* src/dequant.rs:223-254 */
+      const float d = go_h2f(rd16(x)), dmin = go_h2f(rd16(x + 2));
+      const uint8_t* scales = x + 4;
+      const uint8_t* qs = x + 16;
+      for (int g = 0; g < 4; ++g) {
+        int sc, m;
+        scale_min_k4(2 * g, scales, &sc, &m);
+        const float d1 = d * (float)sc, m1 = dmin * (float)m;
+        scale_min_k4(2 * g + 1, scales, &sc, &m);
+        const float d2 = d * (float)sc, m2 = dmin * (float)m;
+        for (int l = 0; l < 32; ++l) {
+          y[64 * g + l] = d1 * (float)(qs[32 * g + l] & 0xF) - m1;
+          y[64 * g + 32 + l] = d2 * (float)(qs[32 * g + l] >> 4) - m2;
+        }
+      }
+    } else { /* Q6_K, src/dequant.rs:296-323 */
+      const uint8_t* ql = x;
+      const uint8_t* qh = x + 128;
+      const int8_t* sc = (const int8_t*)(x + 192);
+      const float d = go_h2f(rd16(x + 208));
+      for (int nh = 0; nh < 2; ++nh) {
+        for (int l = 0; l < 32; ++l) {
+          const int is = l / 16;
+          const uint8_t a = ql[64 * nh + l], bq = ql[64 * nh + l + 32], h = qh[32 * nh + l];
+          const int q1 = (int)((a & 0xF) | ((h & 3) << 4)) - 32;
+          const int q2 = (int)((bq & 0xF) | (((h >> 2) & 3) << 4)) - 32;
+          const int q3 = (int)((a >> 4) | (((h >> 4) & 3) << 4)) - 32;
+          const int q4 = (int)((bq >> 4) | (((h >> 6) & 3) << 4)) - 32;
+          float* ys = y + 128 * nh;
+          ys[l] = d * (float)sc[8 * nh + is] * (float)q1;
+          ys[l + 32] = d * (float)sc[8 * nh + is + 2] * (float)q2;
+          ys[l + 64] = d * (float)sc[8 * nh + is + 4] * (float)q3;
+          ys[l + 96] = d * (float)sc[8 * nh + is + 6] * (float)q4;
+        }
+      }
+    }
+  }
+  return 0;
+}
+
+/* y[r] = sum_k w[r][k] * x[k] (fp64) for rows of K weights stored as ggml
+ * blocks, rows contiguous. */
+int go_gemv_q(int fmt, const uint8_t* blocks, int N, int K, const uint16_t* x, double* y) {
+  const int be = go_qblock_elems(fmt), bb = go_qblock_bytes(fmt);
+  if (bb < 0 || K % be) return -1;
+  float row[16384];
+  if (K > 16384) return -1;
+  const size_t row_bytes = (size_t)(K / be) * (size_t)bb;
+  for (int r = 0; r < N; ++r) {
+    go_dequant(fmt, blocks + (size_t)r * row_bytes, (size_t)K, row);
+    double s = 0.0;
+    for (int k = 0; k < K; ++k) s += (double)row[k] * (double)go_h2f(x[k]);
+    y[r] = s;
+  }
+  return 0;
+}

@@ -13,6 +13,7 @@ __all__ = [
     "splitmix64_at", "inv_freq", "rope_table", "rsqrt_det", "sumsq_row128",
     "qk_norm_rope_row", "qk_norm_rope_kv_prefill", "qk_norm_rope_kv_decode",
     "attention_prefill_rows", "attention_decode", "decode_split", "splitk_merge",
+    "Q8_0", "Q4_K", "Q6_K", "qblock", "dequant", "gemv_q",
     "SEED_BASE", "seed_for",
 ]
 
@@ -32,14 +33,16 @@ def seed_for(tag: str, base: int = SEED_BASE) -> int:
 
 def build(force: bool = False) -> str:
     """Compile the oracle with its Makefile (gcc, -O2, no fast-math, no contraction)."""
-    if force or not os.path.exists(_SO) or (
-        os.path.getmtime(_SO) < os.path.getmtime(os.path.join(_HERE, "grout_oracle.c"))
+    srcs = ("grout_oracle.c", "ggml_quant.c", "Makefile")
+    if force or not os.path.exists(_SO) or any(
+        os.path.getmtime(_SO) < os.path.getmtime(os.path.join(_HERE, f)) for f in srcs
     ):
         subprocess.run(["make", "-s", "-C", _HERE], check=True)
     return _SO
 
 
 _u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
 _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
 _f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
 _i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
@@ -67,6 +70,10 @@ _SIGS = {
     "go_decode_split": (None, [_u16p, _u16p, _u16p, _f32p, _f32p, _i, _i, _i, _i, _l, _f, _i,
                                _i]),
     "go_splitk_merge": (None, [_f32p, _f32p, _f32p, _i, _i, _i, _i]),
+    "go_qblock_bytes": (_i, [_i]),
+    "go_qblock_elems": (_i, [_i]),
+    "go_dequant": (_i, [_i, _u8p, _sz, _f32p]),
+    "go_gemv_q": (_i, [_i, _u8p, _i, _i, _u16p, _f64p]),
 }
 
 
@@ -208,6 +215,32 @@ def decode_split(q, k_cache, v_cache, pos: int, BN: int, NKS: int, scale=None):
     lib().go_decode_split(_u16(q), _u16(k_cache), _u16(v_cache), att, lse, pos, Hq, Hkv, D,
                           k_cache.shape[1] * D, scale, BN, NKS)
     return att, lse
+
+
+Q8_0, Q4_K, Q6_K = 8, 12, 14  # ggml type ids
+
+
+def qblock(fmt: int):
+    """(weights per block, bytes per block) of a ggml quantized format."""
+    return int(lib().go_qblock_elems(fmt)), int(lib().go_qblock_bytes(fmt))
+
+
+def dequant(fmt: int, blocks, n: int) -> np.ndarray:
+    """ggml blocks (uint8) -> n fp32 weights (src/dequant.rs:211-323)."""
+    out = np.empty(n, np.float32)
+    rc = lib().go_dequant(fmt, np.ascontiguousarray(blocks, np.uint8).reshape(-1), n, out)
+    if rc != 0:
+        raise ValueError(f"dequant of format {fmt} with {n} weights failed")
+    return out
+
+
+def gemv_q(fmt: int, blocks, N: int, K: int, x) -> np.ndarray:
+    """y = W x in fp64 for rows of ggml blocks (the quantized GEMV reference)."""
+    y = np.empty(N, np.float64)
+    rc = lib().go_gemv_q(fmt, np.ascontiguousarray(blocks, np.uint8).reshape(-1), N, K, _u16(x), y)
+    if rc != 0:
+        raise ValueError("gemv_q failed")
+    return y
 
 
 def splitk_merge(att, lse, Hq: int) -> np.ndarray:

@@ -1,0 +1,129 @@
+"""CPU pins of the ggml dequantization oracle (oracle/ggml_quant.c).
+
+Each format is checked against blocks built by an independent *encoder*
+written here from the published block layout (the inverse of the decode: a
+wrong bit position, nibble order, scale index or sign in the oracle makes the
+decoded weights differ from the values that were encoded), with the expected
+weights computed in numpy float32 in the reference's operation order."""
+import numpy as np
+import pytest
+
+import oracle as O
+
+F16 = np.float16
+
+
+def f16b(v):
+    return np.array([v], F16).view(np.uint16)[0]
+
+
+def enc_q8_0(d, q):
+    """One Q8_0 block: f16 d then 32 int8."""
+    b = np.zeros(34, np.uint8)
+    b[0:2] = np.array([f16b(d)], np.uint16).view(np.uint8)
+    b[2:] = np.asarray(q, np.int8).view(np.uint8)
+    return b
+
+
+def pack_scale_min_k4(sc, m):
+    """12 bytes holding eight 6-bit (scale, min) pairs: pairs 0-3 in the low 6
+    bits of bytes 0-3 / 4-7, pairs 4-7 split into a low nibble (bytes 8-11)
+    and two high bits (bits 6-7 of bytes 0-3 / 4-7)."""
+    out = np.zeros(12, np.uint8)
+    for j in range(4):
+        out[j] = (sc[j] & 63) | ((sc[j + 4] >> 4) << 6)
+        out[j + 4] = (m[j] & 63) | ((m[j + 4] >> 4) << 6)
+        out[j + 8] = (sc[j + 4] & 0xF) | ((m[j + 4] & 0xF) << 4)
+    return out
+
+
+def enc_q4_k(d, dmin, sc, m, q):
+    """q: 256 values in [0, 15] in weight order."""
+    b = np.zeros(144, np.uint8)
+    b[0:4] = np.array([f16b(d), f16b(dmin)], np.uint16).view(np.uint8)
+    b[4:16] = pack_scale_min_k4(sc, m)
+    q = np.asarray(q)
+    for g in range(4):
+        lo, hi = q[64 * g:64 * g + 32], q[64 * g + 32:64 * g + 64]
+        b[16 + 32 * g:16 + 32 * g + 32] = (lo | (hi << 4)).astype(np.uint8)
+    return b
+
+
+def enc_q6_k(d, sc, q):
+    """q: 256 6-bit values in [0, 63] in weight order (weight = d*sc*(q-32))."""
+    b = np.zeros(210, np.uint8)
+    q = np.asarray(q)
+    ql, qh = b[0:128], b[128:192]
+    for n in range(2):
+        for l in range(32):
+            q1, q2, q3, q4 = (q[128 * n + l + 32 * i] for i in range(4))
+            ql[64 * n + l] = (q1 & 0xF) | ((q3 & 0xF) << 4)
+            ql[64 * n + l + 32] = (q2 & 0xF) | ((q4 & 0xF) << 4)
+            qh[32 * n + l] = (q1 >> 4) | ((q2 >> 4) << 2) | ((q3 >> 4) << 4) | ((q4 >> 4) << 6)
+    b[192:208] = np.asarray(sc, np.int8).view(np.uint8)
+    b[208:210] = np.array([f16b(d)], np.uint16).view(np.uint8)
+    return b
+
+
+def test_block_geometry():
+    assert O.qblock(O.Q8_0) == (32, 34)
+    assert O.qblock(O.Q4_K) == (256, 144)
+    assert O.qblock(O.Q6_K) == (256, 210)
+
+
+def test_q8_0_closed_form():
+    q = np.arange(-16, 16, dtype=np.int8) * 7 // 2
+    got = O.dequant(O.Q8_0, enc_q8_0(0.5, q), 32)
+    assert np.array_equal(got, q.astype(np.float32) * np.float32(0.5))
+    q = np.array([-128, 127] + [0] * 30, np.int8)
+    got = O.dequant(O.Q8_0, enc_q8_0(-0.0078125, q), 32)
+    assert got[0] == 1.0 and got[1] == np.float32(-0.9921875)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_q4_k_against_encoder(seed):
+    rng = np.random.default_rng(seed)
+    d, dmin = F16(rng.uniform(1e-3, 0.1)), F16(rng.uniform(1e-3, 0.1))
+    sc, m = rng.integers(0, 64, 8), rng.integers(0, 64, 8)
+    sc[7], m[4] = 63, 63  # top bits of both halves of the packing
+    q = rng.integers(0, 16, 256)
+    got = O.dequant(O.Q4_K, enc_q4_k(d, dmin, sc, m, q), 256)
+    f32 = np.float32
+    s = np.repeat(sc, 32).astype(f32)
+    mm = np.repeat(m, 32).astype(f32)
+    want = (f32(d) * s) * q.astype(f32) - f32(dmin) * mm
+    assert np.array_equal(got, want.astype(f32))
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_q6_k_against_encoder(seed):
+    rng = np.random.default_rng(10 + seed)
+    d = F16(rng.uniform(1e-3, 0.05))
+    sc = rng.integers(-128, 128, 16)
+    q = rng.integers(0, 64, 256)
+    q[:4] = [0, 63, 32, 31]
+    got = O.dequant(O.Q6_K, enc_q6_k(d, sc, q), 256)
+    f32 = np.float32
+    s = np.repeat(sc, 16).astype(f32)  # 16 weights share a scale, in weight order
+    want = (f32(d) * s) * (q - 32).astype(f32)
+    assert np.array_equal(got, want.astype(f32))
+
+
+def test_gemv_q_is_dequant_times_x():
+    rng = np.random.default_rng(3)
+    N, K = 5, 512
+    rows = [np.concatenate([enc_q4_k(F16(0.01), F16(0.02), rng.integers(0, 64, 8),
+                                     rng.integers(0, 64, 8), rng.integers(0, 16, 256))
+                            for _ in range(K // 256)]) for _ in range(N)]
+    blocks = np.stack(rows)
+    x = rng.standard_normal(K).astype(F16).view(np.uint16)
+    w = O.dequant(O.Q4_K, blocks, N * K).reshape(N, K).astype(np.float64)
+    want = w @ O.h2f(x).astype(np.float64)
+    assert np.allclose(O.gemv_q(O.Q4_K, blocks, N, K, x), want, rtol=0, atol=1e-12)
+
+
+def test_bad_sizes_are_rejected():
+    with pytest.raises(ValueError):
+        O.dequant(O.Q4_K, np.zeros(144, np.uint8), 100)
+    with pytest.raises(ValueError):
+        O.dequant(3, np.zeros(144, np.uint8), 256)
