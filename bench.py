@@ -36,7 +36,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--only", default="",
-                    help="comma list: decode32b,prefill,decode4b,norm,engine4b (gemv: only "
+                    help="comma list: decode32b,prefill,decode4b,norm,engine4b (gemv, qgemv: only "
                          "when named)")
     ap.add_argument("--eager", action="store_true",
                     help="launch the timed calls from the host instead of replaying a captured "
@@ -303,6 +303,62 @@ def bench_gemv(steps, warmup):
     return out
 
 
+def bench_qgemv(steps, warmup):
+    """The low-bit GEMVs (Q8_0 / Q4_K / Q6_K) on the Qwen3-4B decode shapes:
+    random ggml payloads (block scales set to 0.01) repacked once, then timed
+    over enough rotating copies that more than 600 MB of weights cycle (past
+    the 256 MB Infinity Cache).  GB/s counts the repacked weight bytes read
+    per launch plus the f16 input and output."""
+    import ctypes as C
+    import torch
+    from grout_amd._lib import call, lib
+
+    L = lib()
+    dev = torch.device("cuda")
+    H, I, QKV, Q, V = 2560, 9728, 6144, 4096, 151936
+    shapes = {"qkv": (QKV, H, False), "o_proj": (H, Q, False), "gate_up_silu": (2 * I, H, True),
+              "down": (H, I, False), "lm_head": (V, H, False)}
+    fmts = {"Q8_0": (8, 32, 34, 0), "Q4_K": (12, 256, 144, 0), "Q6_K": (14, 256, 210, 208)}
+    P = lambda t: C.c_void_p(t.data_ptr())
+    d_bytes = torch.tensor([0.01], dtype=torch.float16).view(torch.uint8).to(dev)
+    out = {}
+    for fname, (fmt, be, bb, d_off) in fmts.items():
+        res = {}
+        for name, (n, k, silu) in shapes.items():
+            nbytes = L.grout_qweight_bytes(fmt, n, k)
+            copies = max(1, min(8, -(-600_000_000 // nbytes)))
+            Ws = []
+            for c in range(copies):
+                raw = torch.randint(0, 256, (n * k // be, bb), dtype=torch.uint8, device=dev)
+                raw[:, d_off:d_off + 2] = d_bytes
+                if fmt == 12:
+                    raw[:, 2:4] = d_bytes
+                w = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+                call("grout_qweight_repack", fmt, P(raw), n, k, P(w), None)
+                Ws.append(w)
+                del raw
+            x = (torch.randn(k, device=dev) * 0.1).to(torch.float16)
+            y = torch.empty(n, dtype=torch.float16, device=dev)
+
+            def fn(i, Ws=Ws, x=x, y=y, n=n, k=k, silu=silu, fmt=fmt):
+                s = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+                if silu:
+                    call("grout_gemv_q_silu_mul", fmt, P(Ws[i % len(Ws)]), P(x), P(y), n // 2, k, s)
+                else:
+                    call("grout_gemv_q", fmt, P(Ws[i % len(Ws)]), P(x), P(y), n, k, s)
+
+            ms = time_launches(fn, steps, warmup)
+            moved = nbytes + 2 * k + 2 * (n // 2 if silu else n)
+            res[name] = dict(us=round(ms * 1e3, 2), gbs=round(moved / (ms * 1e-3) / 1e9, 1),
+                             weight_bytes=nbytes)
+            del Ws
+            torch.cuda.empty_cache()
+        res["step_weight_us"] = round(36 * sum(res[s]["us"] for s in ("qkv", "o_proj", "gate_up_silu",
+                                                                       "down")) + res["lm_head"]["us"], 1)
+        out[fname] = res
+    return out
+
+
 def cpu_baseline_decode(Hq, Hkv, ctx):
     """Scalar fp32 oracle (single thread) on one 32B decode layer: 16 of the 64
     query heads (2 kv heads) at full context; GB/s scaled to the whole layer."""
@@ -373,6 +429,9 @@ def main():
     if "gemv" in only:
         res["gemv"] = bench_gemv(a.steps, a.warmup)
         print(f"# gemv {res['gemv']}", file=sys.stderr, flush=True)
+    if "qgemv" in only:
+        res["qgemv"] = bench_qgemv(a.steps, a.warmup)
+        print(f"# qgemv {res['qgemv']}", file=sys.stderr, flush=True)
     if want("engine4b"):
         res["engine4b"] = bench_engine()
         # attention part of one decode step at the mean context of the run:
@@ -421,6 +480,8 @@ def main():
                                    "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
     if "gemv" in res:
         line["gemv"] = res["gemv"]
+    if "qgemv" in res:
+        line["qgemv"] = res["qgemv"]
     if "engine4b" in res:
         r = res["engine4b"]
         gbs = r["bytes_per_token"] * r["tok_s"] / 1e9

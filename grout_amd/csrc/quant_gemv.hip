@@ -15,26 +15,19 @@
 //         h  16 B [N][K/256] (d, dmin, the 12 packed 6-bit scale/min bytes)
 //   Q6_K: ql u8 [N][K/2], qh u8 [N][K/4], sc int8 [N][K/16], d f16 [N][K/256]
 //
-// Kernel: a 256-thread workgroup owns 16 weight rows (for SiLU pairs: 8 gate
-// rows and their 8 up rows) and stages x in LDS.  The rows are cut into
-// 16-byte pieces of the primary payload (Q8_0: 16 weights; Q4_K / Q6_K: 32
-// weights as two runs of 16) and the threads take pieces round robin; each
-// thread issues all weight loads of a batch before it consumes any.  A run of
-// 16 quantized values becomes exact f16 integers (byte | 0x6400 is the f16
-// 1024 + byte), its dot product with x uses v_dot2_f32_f16, and the run's
-// scale (and min) is applied once: scale * sum(q x) - min * sum(x).  Partial
-// sums go to LDS per piece and each row is summed in a fixed order, so the
-// result does not depend on scheduling.
+// GEMV kernel: one 16-lane team per weight row, x and the rows' decoded
+// block scales staged in LDS (swizzled against bank conflicts), the weights
+// streamed with every load of a lane in flight before its first use.  A run
+// of 16 quantized values becomes exact f16 integers (v_perm inserts 0x64, the
+// exponent byte of 1024, above each byte; a packed subtract removes 1024 plus
+// the format's offset), its dot product with x uses v_dot2_f32_f16, and the
+// run's scale (and min) is applied once: scale * sum(q x) - min * sum(x).
 #include "common.hpp"
 #include "kernels.hpp"
 
 namespace grout {
 
-constexpr int kQRows = 16;        // weight rows per workgroup
-constexpr int kQThreads = 256;
-constexpr int kQBatch = 8;        // pieces per thread issued before any is consumed
-constexpr int kQMaxK = 16384;     // x staged in LDS (at most 32 KiB)
-constexpr int kQMaxPieces = 16 * 1024;  // kQRows x pieces per row (at most 64 KiB of fp32)
+constexpr int kQMaxK = 16384;  // x staged in LDS (at most 32 KiB)
 
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
@@ -105,45 +98,415 @@ __global__ __launch_bounds__(256) void qrepack_kernel(int fmt, const uint8_t* __
   }
 }
 
-// ---------------------------------------------------------------- piece decode
+// ---------------------------------------------------------------- GEMV
+//
+// A row team of 16 lanes owns one weight row; lane m takes the row's pieces
+// p = m, m + 16, ... (a piece is 32 consecutive weights: Q8_0 one block;
+// Q4_K 16 qs bytes = 16 weights of sub-block 2g in the low nibbles and 16 of
+// 2g+1 in the high; Q6_K 16 ql bytes and the 16 qh bytes they pair with), so a
+// team reads 256 contiguous bytes per load and p % 8 == m % 8 fixes each
+// lane's place inside a superblock.  Workgroups of R teams (4 for short
+// matrices so the grid covers every CU, 16 for tall ones); before the
+// barrier a workgroup stages x and its rows' decoded block scales in LDS,
+// with those loads issued ahead of the weight loads.  Each lane sums its
+// pieces in order and the team reduces with a fixed butterfly, so results do
+// not depend on scheduling.
 
-// Four bytes (each an integer 0..255) -> two f16 pairs holding (1024 + byte);
-// `bias` is subtracted exactly (1024 for unsigned values, 1152 for int8 that
-// were offset by 128, 1056 for 6-bit values stored with +32).
-__device__ __forceinline__ void bytes_to_f16(uint32_t v, half2v bias, half2v& lo, half2v& hi) {
-  const uint32_t a = (v & 0xFFu) | ((v & 0xFF00u) << 8) | 0x64006400u;
-  const uint32_t b = ((v >> 16) & 0xFFu) | ((v >> 8) & 0xFF0000u) | 0x64006400u;
-  lo = __builtin_bit_cast(half2v, a) - bias;
-  hi = __builtin_bit_cast(half2v, b) - bias;
+constexpr int kQTeam = 16;  // lanes per weight row
+
+__device__ __forceinline__ float h2f_bits(uint16_t b) { return (float)__builtin_bit_cast(half_t, b); }
+
+// LDS granule (8 halves of x) for logical granule G.  Lane m of a team reads
+// granules whose bits 1-5 are functions of m; the map moves the lane-varying
+// bits onto bits 0-3 so any 8 or 16 lanes of a team hit distinct bank
+// groups.  Linear over GF(2), confined to aligned runs of 16 granules and
+// blind to bits 6 and up: xswz(G + 64 i) = xswz(G) + 64 i.
+template <int FMT>
+__host__ __device__ constexpr int xswz(int G) {
+  return FMT == 8    ? G ^ ((G >> 3) & 3) ^ (((G >> 5) & 1) << 3)
+         : FMT == 12 ? G ^ ((G >> 3) & 1) ^ (((G >> 4) & 1) << 2) ^ (((G >> 5) & 1) << 3)
+                     : G ^ ((G >> 4) & 1) ^ (((G >> 5) & 1) << 3);
 }
 
-// sum over 16 values: q (4 words of 4 bytes, bias removed) . x (16 f16)
-__device__ __forceinline__ float dot16(const uint32_t (&w)[4], half2v bias, const half8& x0,
-                                       const half8& x1, float acc) {
+// Slot of 16-run r in the Q4_K x sums (runs r and r + 2 of one piece side by
+// side) and in the Q6_K scales and x sums (runs r and r + 4 side by side).
+__host__ __device__ constexpr int xsum_slot(int r) { return (r & ~3) | ((r & 1) << 1) | ((r >> 1) & 1); }
+__host__ __device__ constexpr int q6_slot(int r) { return (r & ~7) | ((r & 3) << 1) | ((r >> 2) & 1); }
+
+// Weight row of local row lr and the output it feeds.  SILU: in each wave the
+// teams are gate rows o, o+1 then the up rows o, o+1 (up row = N + o).
+template <bool SILU, int R>
+__device__ __forceinline__ int qrow(int lr, int N, int& out) {
+  if (SILU) {
+    const int t = lr & 3;
+    out = (int)blockIdx.x * (R / 2) + 2 * (lr >> 2) + (t & 1);
+    const int o = min(out, N - 1);
+    return t < 2 ? o : N + o;
+  }
+  out = (int)blockIdx.x * R + lr;
+  return min(out, N - 1);
+}
+
+// Raw bytes of one piece.
+struct QPc {
+  u32x4 a;  // Q8_0 q[0..15]; Q4_K qs; Q6_K ql
+  u32x4 b;  // Q8_0 q[16..31]; Q6_K qh
+};
+
+template <int FMT>
+__device__ __forceinline__ QPc qpc_load(const uint8_t* __restrict__ W, const QLayout& L, int row,
+                                        int p, int K) {
+  QPc r;
+  if (FMT == 8) {
+    const uint8_t* q = W + L.off[0] + (size_t)row * K + (size_t)p * 32;
+    r.a = load_stream16(q);
+    r.b = load_stream16(q + 16);
+  } else if (FMT == 12) {
+    r.a = load_stream16(W + L.off[0] + (size_t)row * (K / 2) + (size_t)p * 16);
+    r.b = r.a;
+  } else {
+    r.a = load_stream16(W + L.off[0] + (size_t)row * (K / 2) + (size_t)p * 16);
+    // qh bytes 32n + 16 l0 .. +15 of superblock p / 8 (n = bit 2 of p, l0 = bit 0)
+    r.b = load_stream16(W + L.off[1] + (size_t)row * (K / 4) + (size_t)(p >> 3) * 64 +
+                        ((p >> 2) & 1) * 32 + (p & 1) * 16);
+  }
+  return r;
+}
+
+// Two bytes of v as an f16 pair of denormals, byte * 2^-24 (exact; v_perm
+// selector 0x0C is a zero byte): sel 0x0C010C00 takes bytes 0, 1 and
+// 0x0C030C02 bytes 2, 3.
+__device__ __forceinline__ half2v dpair(uint32_t v, uint32_t sel) {
+  return __builtin_bit_cast(half2v, __builtin_amdgcn_perm(v, v, sel));
+}
+
+// acc + 2^-24 * sum_t byte_t * x_t over the 16 little-endian bytes of w and
+// x0 (t < 8), x1: products of f16 values are exact in the fp32 accumulation.
+__device__ __forceinline__ float ddot16(const uint32_t (&w)[4], half8 x0, half8 x1, float acc) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    half2v lo, hi;
-    bytes_to_f16(w[i], bias, lo, hi);
     const half8& xs = i < 2 ? x0 : x1;
     const int e = (i & 1) * 4;
-    acc = __builtin_amdgcn_fdot2(lo, half2v{xs[e], xs[e + 1]}, acc, false);
-    acc = __builtin_amdgcn_fdot2(hi, half2v{xs[e + 2], xs[e + 3]}, acc, false);
+    acc = __builtin_amdgcn_fdot2(dpair(w[i], 0x0C010C00u), half2v{xs[e], xs[e + 1]}, acc, false);
+    acc = __builtin_amdgcn_fdot2(dpair(w[i], 0x0C030C02u), half2v{xs[e + 2], xs[e + 3]}, acc,
+                                 false);
   }
   return acc;
 }
 
-__device__ __forceinline__ float sum16(const half8& x0, const half8& x1) {
+// Per-lane LDS offsets for piece i = 0 (piece i adds 64 i granules, and 16 i
+// (Q8_0) or 32 i (Q4_K, Q6_K) floats of scales and x sums).
+struct QLane {
+  int xg[4];  // byte offsets of the x granules: Q8_0 4 of one run; else lo, lo+1, hi, hi+1
+  int so;     // float offset into the row's scales
+  int xo;     // float offset into the x sums
+};
+
+template <int FMT>
+__device__ __forceinline__ QLane qlane(int m) {
+  QLane q;
+  if (FMT == 8) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) q.xg[k] = 16 * xswz<FMT>(4 * m + k);
+    q.so = q.xo = m;
+  } else if (FMT == 12) {
+    // lo run: weights 256 sb + 64 g + 16 l0 (sub-block 2g), hi run +32 (2g+1)
+    const int g = (m >> 1) & 3, l0 = m & 1, s3 = m >> 3;
+    const int G = 32 * s3 + 8 * g + 2 * l0;
+    q.xg[0] = 16 * xswz<FMT>(G);
+    q.xg[1] = 16 * xswz<FMT>(G + 1);
+    q.xg[2] = 16 * xswz<FMT>(G + 4);
+    q.xg[3] = 16 * xswz<FMT>(G + 5);
+    q.so = 16 * s3 + 4 * g;
+    q.xo = 16 * s3 + 4 * g + 2 * l0;
+  } else {
+    // lo run: weights 256 sb + 128 n + 32 ilo + 16 l0 (qh bits 2 ilo), hi run
+    // +64 (qh bits 2 ilo + 4)
+    const int n = (m >> 2) & 1, ilo = (m >> 1) & 1, l0 = m & 1, s3 = m >> 3;
+    const int G = 32 * s3 + 16 * n + 4 * ilo + 2 * l0;
+    q.xg[0] = 16 * xswz<FMT>(G);
+    q.xg[1] = 16 * xswz<FMT>(G + 1);
+    q.xg[2] = 16 * xswz<FMT>(G + 8);
+    q.xg[3] = 16 * xswz<FMT>(G + 9);
+    q.so = q.xo = q6_slot(16 * s3 + 8 * n + 2 * ilo + l0);
+  }
+  return q;
+}
+
+template <int I>
+__device__ __forceinline__ half8 xgran(const unsigned char* s_xb, int off) {
+  return *reinterpret_cast<const half8*>(s_xb + off + 1024 * I);
+}
+
+// Contribution of piece i of lane m (piece index p = m + 16 i) to the row's
+// dot product.  Staged scales carry the 2^24 of the denormal encoding.
+template <int FMT, int I>
+__device__ __forceinline__ float qpc_dot(const QPc& r, int m, const QLane& q,
+                                         const unsigned char* s_xb, const float* s_xsum,
+                                         const float* s_row) {
+  if (FMT == 8) {
+    // bytes hold q + 128: sum (q + 128) x - 128 sum x
+    const uint32_t wa[4] = {r.a[0] ^ 0x80808080u, r.a[1] ^ 0x80808080u, r.a[2] ^ 0x80808080u,
+                            r.a[3] ^ 0x80808080u};
+    const uint32_t wb[4] = {r.b[0] ^ 0x80808080u, r.b[1] ^ 0x80808080u, r.b[2] ^ 0x80808080u,
+                            r.b[3] ^ 0x80808080u};
+    const float da = ddot16(wa, xgran<I>(s_xb, q.xg[0]), xgran<I>(s_xb, q.xg[1]), 0.f);
+    const float db = ddot16(wb, xgran<I>(s_xb, q.xg[2]), xgran<I>(s_xb, q.xg[3]), 0.f);
+    return s_row[q.so + 16 * I] * ((da + db) - s_xsum[q.xo + 16 * I]);
+  } else if (FMT == 12) {
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      lo[i] = r.a[i] & 0x0F0F0F0Fu;
+      hi[i] = r.a[i] & 0xF0F0F0F0u;  // 16 x the high nibble
+    }
+    const float dlo = ddot16(lo, xgran<I>(s_xb, q.xg[0]), xgran<I>(s_xb, q.xg[1]), 0.f);
+    const float dhi = ddot16(hi, xgran<I>(s_xb, q.xg[2]), xgran<I>(s_xb, q.xg[3]), 0.f);
+    // {2^24 d sc_2g, dmin m_2g, 2^20 d sc_2g+1, dmin m_2g+1}
+    const floatx4 sc = *reinterpret_cast<const floatx4*>(s_row + q.so + 32 * I);
+    const float2 xs = *reinterpret_cast<const float2*>(s_xsum + q.xo + 32 * I);
+    return (sc[0] * dlo - sc[1] * xs.x) + (sc[2] * dhi - sc[3] * xs.y);
+  } else {
+    // 6-bit q held + 32: sum (q + 32) x - 32 sum x per run
+    const int ilo = (m >> 1) & 1;
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      lo[i] = (r.a[i] & 0x0F0F0F0Fu) | ((r.b[i] << (4 - 2 * ilo)) & 0x30303030u);
+      hi[i] = ((r.a[i] >> 4) & 0x0F0F0F0Fu) | ((r.b[i] >> (2 * ilo)) & 0x30303030u);
+    }
+    const float dlo = ddot16(lo, xgran<I>(s_xb, q.xg[0]), xgran<I>(s_xb, q.xg[1]), 0.f);
+    const float dhi = ddot16(hi, xgran<I>(s_xb, q.xg[2]), xgran<I>(s_xb, q.xg[3]), 0.f);
+    const float2 s = *reinterpret_cast<const float2*>(s_row + q.so + 32 * I);
+    const float2 xs = *reinterpret_cast<const float2*>(s_xsum + q.xo + 32 * I);
+    return s.x * (dlo - xs.x) + s.y * (dhi - xs.y);
+  }
+}
+
+// Staging of x: granule c to its swizzled slot, and the x sum of each run
+// (Q8_0: 32-runs = granules c..c+3, scaled by 128 * 2^-24; Q4_K: 16-runs;
+// Q6_K: 16-runs scaled by 32 * 2^-24), the run's granules sitting in
+// adjacent lanes.  Every lane calls it.
+template <int FMT>
+__device__ __forceinline__ void stage_x(u32x4 v, int c, int NG, half_t* s_x, float* s_xsum) {
+  const half8 h = as_half8(v);
   const half2v one = {(half_t)1.0f, (half_t)1.0f};
   float s = 0.f;
 #pragma unroll
-  for (int e = 0; e < 8; e += 2) {
-    s = __builtin_amdgcn_fdot2(half2v{x0[e], x0[e + 1]}, one, s, false);
-    s = __builtin_amdgcn_fdot2(half2v{x1[e], x1[e + 1]}, one, s, false);
+  for (int e = 0; e < 8; e += 2) s = __builtin_amdgcn_fdot2(half2v{h[e], h[e + 1]}, one, s, false);
+  s += __shfl_xor(s, 1, 64);
+  if (FMT == 8) {
+    s += __shfl_xor(s, 2, 64);
+    if (c < NG && (c & 3) == 0) s_xsum[c >> 2] = s * 0x1p-17f;
+  } else if (FMT == 12) {
+    if (c < NG && (c & 1) == 0) s_xsum[xsum_slot(c >> 1)] = s;
+  } else {
+    if (c < NG && (c & 1) == 0) s_xsum[q6_slot(c >> 1)] = s * 0x1p-19f;
+  }
+  if (c < NG) *reinterpret_cast<u32x4*>(s_x + 8 * xswz<FMT>(c)) = v;
+}
+
+// One staging unit: Q8_0 one block scale; Q4_K one superblock header; Q6_K
+// one superblock's 16 scales and d.
+struct SRaw {
+  u32x4 v;
+  uint32_t d;
+};
+
+template <int FMT, bool SILU, int R>
+__device__ __forceinline__ SRaw stage_load(const uint8_t* __restrict__ W, const QLayout& L, int u,
+                                           int UPR, int N, int K) {
+  const int lr = u / UPR, k = u - lr * UPR;
+  int o;
+  const int row = qrow<SILU, R>(lr, N, o);
+  SRaw s;
+  s.v = u32x4{0u, 0u, 0u, 0u};
+  s.d = 0;
+  if (FMT == 8) {
+    s.d = *reinterpret_cast<const uint16_t*>(W + L.off[1] + ((size_t)row * (K / 32) + k) * 2);
+  } else if (FMT == 12) {
+    s.v = load16(W + L.off[1] + ((size_t)row * (K / 256) + k) * 16);
+  } else {
+    s.v = load16(W + L.off[2] + (size_t)row * (K / 16) + (size_t)k * 16);
+    s.d = *reinterpret_cast<const uint16_t*>(W + L.off[3] + ((size_t)row * (K / 256) + k) * 2);
   }
   return s;
 }
 
-__device__ __forceinline__ float h2f_bits(uint16_t b) { return (float)__builtin_bit_cast(half_t, b); }
+// Scales in fp32 as the reference forms them (d * sc, dmin * m), then times
+// the power of two that undoes the denormal encoding (exact).
+template <int FMT>
+__device__ __forceinline__ void stage_store(const SRaw& s, int u, int U, int UPR, int SCW,
+                                            float* s_sc) {
+  if (u >= U) return;
+  const int lr = u / UPR, k = u - lr * UPR;
+  float* dst = s_sc + lr * SCW;
+  if (FMT == 8) {
+    dst[k] = h2f_bits((uint16_t)s.d) * 0x1p24f;
+  } else if (FMT == 12) {
+    // d, dmin, then eight 6-bit (scale, min) pairs packed in 12 bytes
+    const float d = h2f_bits((uint16_t)(s.v[0] & 0xFFFFu));
+    const float dmin = h2f_bits((uint16_t)(s.v[0] >> 16));
+    int q[12];
+#pragma unroll
+    for (int j = 0; j < 12; ++j) q[j] = (s.v[1 + j / 4] >> (8 * (j % 4))) & 0xFF;
+    int sc[8], mn[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (j < 4) {
+        sc[j] = q[j] & 63;
+        mn[j] = q[j + 4] & 63;
+      } else {
+        sc[j] = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        mn[j] = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      *reinterpret_cast<floatx4*>(dst + 16 * k + 4 * g) =
+          floatx4{(d * (float)sc[2 * g]) * 0x1p24f, dmin * (float)mn[2 * g],
+                  (d * (float)sc[2 * g + 1]) * 0x1p20f, dmin * (float)mn[2 * g + 1]};
+  } else {
+    const float d = h2f_bits((uint16_t)s.d);
+    float f[16];
+#pragma unroll
+    for (int t = 0; t < 16; ++t)
+      f[q6_slot(t)] = (d * (float)(int8_t)((s.v[t / 4] >> (8 * (t % 4))) & 0xFF)) * 0x1p24f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<floatx4*>(dst + 16 * k + 4 * i) =
+          floatx4{f[4 * i], f[4 * i + 1], f[4 * i + 2], f[4 * i + 3]};
+  }
+}
+
+// Weight loads in flight per lane (NPW: pieces per lane and slice, 0 = any K).
+template <int FMT, int R, int NPW>
+constexpr int qbatch() {
+  constexpr int cap = R == 4 ? (FMT == 12 ? 20 : 10) : (FMT == 12 ? 8 : 4);
+  return NPW > 0 && NPW < cap ? NPW : cap;
+}
+
+// Consumes pieces st + J.. of the lane's slice (counted from piece i0 on),
+// refilling each slot B pieces ahead.
+template <int FMT, int NPW, int B, int J>
+__device__ __forceinline__ void qconsume(QPc (&raw)[B], float& acc, int st, int i0, int m,
+                                         const QLane& q, const unsigned char* s_xb,
+                                         const float* s_xsum, const float* s_row,
+                                         const uint8_t* __restrict__ W, const QLayout& L, int row,
+                                         int K) {
+  if constexpr (J < NPW) {
+    // the LDS offsets of piece st + J are compile-time steps from the base
+    // pointers, which already point at piece st
+    const float v = qpc_dot<FMT, J>(raw[J % B], m, q, s_xb, s_xsum, s_row);
+    acc += st + J >= i0 ? v : 0.f;
+    if constexpr (J + B < NPW) raw[J % B] = qpc_load<FMT>(W, L, row, m + 16 * (st + J + B), K);
+    qconsume<FMT, NPW, B, J + 1>(raw, acc, st, i0, m, q, s_xb, s_xsum, s_row, W, L, row, K);
+  }
+}
+
+// R weight rows per workgroup, each split into S slices of NPW pieces per
+// lane (one slice per group of R teams; K a multiple of 512 with
+// NPW * S >= K / 512 >= NPW), or NPW = 0: any K, S = 1.
+template <int FMT, bool SILU, int R, int S, int NPW>
+__global__ __launch_bounds__(R * S * kQTeam) void gemv_q_kernel(const uint8_t* __restrict__ W,
+                                                               const half_t* __restrict__ x,
+                                                               half_t* __restrict__ y, int N,
+                                                               int K, QLayout L) {
+  constexpr int T = R * S * kQTeam;
+  constexpr int B = qbatch<FMT, R, NPW>();
+  // LDS: x (K halves, padded to whole swizzle runs), x sums, each local row's
+  // scales (SCW floats), then S x R slice partials.
+  extern __shared__ __attribute__((aligned(16))) unsigned char s_dyn[];
+  const int KX = (K + 127) & ~127;
+  half_t* const s_x = reinterpret_cast<half_t*>(s_dyn);
+  float* const s_xsum = reinterpret_cast<float*>(s_dyn + (size_t)KX * 2);
+  float* const s_sc = s_xsum + (FMT == 8 ? K / 32 : K / 16);
+  const int SCW = FMT == 8 ? K / 32 : K / 16;
+  const int UPR = FMT == 8 ? K / 32 : K / 256;  // staging units per row
+  const int U = R * UPR, NG = K / 8, P = K / 32;
+  const int tid = threadIdx.x, slice = tid / (R * kQTeam), team = (tid >> 4) % R, m = tid & 15;
+  int out;
+  const int row = qrow<SILU, R>(team, N, out);
+  const float* const s_row = s_sc + team * SCW;
+  const QLane q = qlane<FMT>(m);
+  float acc = 0.f;
+
+  if constexpr (NPW > 0) {
+    // x, scale and first weight loads all in flight before any is used (the
+    // per-thread counts are bounds: NP <= NPW * S pieces per lane)
+    constexpr int NXJ = (NPW * S * 64 + T - 1) / T;
+    constexpr int NUJ = ((FMT == 8 ? 16 : 2) * R * NPW * S + T - 1) / T;
+    const int NP = K / 512;
+    // slice pieces i0 .. i0 + NPW - 1 clipped to NP: a slice that would run
+    // past the end starts at NP - NPW and counts only pieces >= i0
+    const int i0 = slice * NPW, st = min(i0, NP - NPW);
+    u32x4 xr[NXJ];
+#pragma unroll
+    for (int j = 0; j < NXJ; ++j) xr[j] = load16(x + 8 * min(tid + T * j, NG - 1));
+    SRaw ur[NUJ];
+#pragma unroll
+    for (int j = 0; j < NUJ; ++j)
+      ur[j] = stage_load<FMT, SILU, R>(W, L, min(tid + T * j, U - 1), UPR, N, K);
+    QPc raw[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) raw[b] = qpc_load<FMT>(W, L, row, m + 16 * (st + b), K);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < NXJ; ++j) stage_x<FMT>(xr[j], tid + T * j, NG, s_x, s_xsum);
+#pragma unroll
+    for (int j = 0; j < NUJ; ++j) stage_store<FMT>(ur[j], tid + T * j, U, UPR, SCW, s_sc);
+    __syncthreads();
+    const int fs = FMT == 8 ? 16 : 32;  // scale / x-sum floats per piece step
+    qconsume<FMT, NPW, B, 0>(raw, acc, st, i0, m, q,
+                             reinterpret_cast<const unsigned char*>(s_x) + 1024 * st,
+                             s_xsum + fs * st, s_row + fs * st, W, L, row, K);
+  } else {
+    const int nxj = (NG + T - 1) / T;
+    for (int j = 0; j < nxj; ++j) {
+      const int c = tid + T * j;
+      stage_x<FMT>(load16(x + 8 * min(c, NG - 1)), c, NG, s_x, s_xsum);
+    }
+    for (int u = tid; u < U; u += T)
+      stage_store<FMT>(stage_load<FMT, SILU, R>(W, L, u, UPR, N, K), u, U, UPR, SCW, s_sc);
+    __syncthreads();
+    const int npl = (P + 15) / 16;
+    const int fs = FMT == 8 ? 16 : 32;
+    const unsigned char* s_xb = reinterpret_cast<const unsigned char*>(s_x);
+    for (int i = 0; i < npl; ++i) {
+      const int p = m + 16 * i;
+      const QPc r = qpc_load<FMT>(W, L, row, min(p, P - 1), K);
+      const float v = qpc_dot<FMT, 0>(r, m, q, s_xb + 1024 * i, s_xsum + fs * i, s_row + fs * i);
+      acc += p < P ? v : 0.f;
+    }
+  }
+
+#pragma unroll
+  for (int off = 8; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 16);
+  if constexpr (S > 1) {
+    // slice partials summed in slice order by slice 0
+    float* const s_red = s_sc + R * SCW;
+    if (m == 0) s_red[slice * R + team] = acc;
+    __syncthreads();
+    if (slice != 0) return;
+    acc = s_red[team];
+#pragma unroll
+    for (int w = 1; w < S; ++w) acc += s_red[w * R + team];
+  }
+  if (SILU) {
+    const float up = __shfl_xor(acc, 32, 64);  // gate teams 0, 1 <-> up teams 2, 3
+    if (m == 0 && (team & 3) < 2 && out < N) {
+      const half_t g = (half_t)acc, u = (half_t)up;
+      const float gf = (float)g;
+      const float sig = 1.0f / (1.0f + expf(-gf));
+      y[out] = (half_t)(sig * gf * (float)u);
+    }
+  } else if (m == 0 && out < N) {
+    y[out] = (half_t)acc;
+  }
+}
+
+// ---------------------------------------------------------------- dequant to f16
+
 
 // Raw bytes of one piece (row, j).
 struct QRaw {
@@ -167,169 +530,6 @@ __device__ __forceinline__ QRaw qload(const uint8_t* __restrict__ W, const QLayo
   return r;
 }
 
-// Contribution of piece j of `row` with its raw bytes, x staged in LDS.
-template <int FMT>
-__device__ __forceinline__ float qpiece(const QRaw& r, const uint8_t* __restrict__ W,
-                                        const QLayout& L, int row, int j, int K,
-                                        const half_t* __restrict__ xs) {
-  if (FMT == 8) {
-    // 16 int8 weights k = 16j .. 16j+15, block j/2
-    const half8 x0 = *reinterpret_cast<const half8*>(xs + 16 * j);
-    const half8 x1 = *reinterpret_cast<const half8*>(xs + 16 * j + 8);
-    uint32_t w[4] = {r.a[0] ^ 0x80808080u, r.a[1] ^ 0x80808080u, r.a[2] ^ 0x80808080u,
-                     r.a[3] ^ 0x80808080u};
-    const half2v bias = {(half_t)1152.0f, (half_t)1152.0f};
-    const float dot = dot16(w, bias, x0, x1, 0.f);
-    const uint16_t db = *reinterpret_cast<const uint16_t*>(W + L.off[1] +
-                                                           ((size_t)row * (K / 32) + (j >> 1)) * 2);
-    return h2f_bits(db) * dot;
-  } else if (FMT == 12) {
-    const int sb = j >> 3, g = (j & 7) >> 1, l0 = (j & 1) * 16;
-    const int e0 = sb * 256 + 64 * g + l0;
-    const half8 xl0 = *reinterpret_cast<const half8*>(xs + e0);
-    const half8 xl1 = *reinterpret_cast<const half8*>(xs + e0 + 8);
-    const half8 xh0 = *reinterpret_cast<const half8*>(xs + e0 + 32);
-    const half8 xh1 = *reinterpret_cast<const half8*>(xs + e0 + 40);
-    uint32_t lo[4], hi[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      lo[i] = r.a[i] & 0x0F0F0F0Fu;
-      hi[i] = (r.a[i] >> 4) & 0x0F0F0F0Fu;
-    }
-    const half2v bias = {(half_t)1024.0f, (half_t)1024.0f};
-    const float dlo = dot16(lo, bias, xl0, xl1, 0.f);
-    const float dhi = dot16(hi, bias, xh0, xh1, 0.f);
-    // header: d, dmin, then the packed 6-bit (scale, min) of sub-blocks 2g, 2g+1
-    const uint8_t* hb = W + L.off[1] + ((size_t)row * (K / 256) + sb) * 16;
-    const u32x4 hv = *reinterpret_cast<const u32x4*>(hb);
-    const uint8_t* sc = reinterpret_cast<const uint8_t*>(&hv) + 4;
-    const float d = h2f_bits((uint16_t)(hv[0] & 0xFFFF)), dmin = h2f_bits((uint16_t)(hv[0] >> 16));
-    int s1, m1, s2, m2;
-    const int j1 = 2 * g, j2 = 2 * g + 1;
-    if (j1 < 4) {
-      s1 = sc[j1] & 63;
-      m1 = sc[j1 + 4] & 63;
-    } else {
-      s1 = (sc[j1 + 4] & 0xF) | ((sc[j1 - 4] >> 6) << 4);
-      m1 = (sc[j1 + 4] >> 4) | ((sc[j1] >> 6) << 4);
-    }
-    if (j2 < 4) {
-      s2 = sc[j2] & 63;
-      m2 = sc[j2 + 4] & 63;
-    } else {
-      s2 = (sc[j2 + 4] & 0xF) | ((sc[j2 - 4] >> 6) << 4);
-      m2 = (sc[j2 + 4] >> 4) | ((sc[j2] >> 6) << 4);
-    }
-    const float d1 = d * (float)s1, mn1 = dmin * (float)m1;
-    const float d2 = d * (float)s2, mn2 = dmin * (float)m2;
-    return (d1 * dlo - mn1 * sum16(xl0, xl1)) + (d2 * dhi - mn2 * sum16(xh0, xh1));
-  } else {
-    const int sb = j >> 3, o = (j & 7) * 16, n = o >> 6, h = o & 63;
-    const int base = sb * 256 + 128 * n + (h & 31);
-    // h < 32: runs i = 0 (ql low, qh bits 0-1) and i = 2 (ql high, bits 4-5);
-    // h >= 32: runs i = 1 (bits 2-3) and i = 3 (bits 6-7)
-    const int ilo = h < 32 ? 0 : 1, ihi = ilo + 2;
-    const int e_lo = base + 32 * ilo, e_hi = base + 32 * ihi;
-    const half8 xl0 = *reinterpret_cast<const half8*>(xs + e_lo);
-    const half8 xl1 = *reinterpret_cast<const half8*>(xs + e_lo + 8);
-    const half8 xh0 = *reinterpret_cast<const half8*>(xs + e_hi);
-    const half8 xh1 = *reinterpret_cast<const half8*>(xs + e_hi + 8);
-    uint32_t lo[4], hi[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      lo[i] = (r.a[i] & 0x0F0F0F0Fu) | (((r.b[i] >> (2 * ilo)) & 0x03030303u) << 4);
-      hi[i] = ((r.a[i] >> 4) & 0x0F0F0F0Fu) | (((r.b[i] >> (2 * ihi)) & 0x03030303u) << 4);
-    }
-    const half2v bias = {(half_t)1056.0f, (half_t)1056.0f};  // 1024 + 32: q - 32
-    const float dlo = dot16(lo, bias, xl0, xl1, 0.f);
-    const float dhi = dot16(hi, bias, xh0, xh1, 0.f);
-    const int8_t* scp = reinterpret_cast<const int8_t*>(W + L.off[2] + (size_t)row * (K / 16));
-    const float d = h2f_bits(
-        *reinterpret_cast<const uint16_t*>(W + L.off[3] + ((size_t)row * (K / 256) + sb) * 2));
-    const float s_lo = d * (float)scp[(e_lo - 0) / 16];
-    const float s_hi = d * (float)scp[(e_hi - 0) / 16];
-    return s_lo * dlo + s_hi * dhi;
-  }
-}
-
-// ---------------------------------------------------------------- GEMV
-
-// SILU: rows are 8 gate rows g0.. and their up rows N + g0.. (N = outputs);
-// otherwise 16 consecutive rows.  pieces per row P = K / (FMT == 8 ? 16 : 32).
-template <int FMT, bool SILU>
-__global__ __launch_bounds__(kQThreads) void gemv_q_kernel(const uint8_t* __restrict__ W,
-                                                          const half_t* __restrict__ x,
-                                                          half_t* __restrict__ y, int N, int K,
-                                                          QLayout L) {
-  // Dynamic LDS: x (K halves), then one fp32 partial per piece (kQRows x P).
-  extern __shared__ __attribute__((aligned(16))) unsigned char s_dyn[];
-  half_t* const s_x = reinterpret_cast<half_t*>(s_dyn);
-  float* const s_part = reinterpret_cast<float*>(s_dyn + (size_t)K * 2);
-  const int tid = threadIdx.x;
-  const int P = K / (FMT == 8 ? 16 : 32);
-  const int total = kQRows * P;
-  const int out0 = blockIdx.x * (SILU ? kQRows / 2 : kQRows);
-  // Local row lr -> weight row (clamped to a valid row; its output is dropped).
-  auto row_of = [&](int lr) __attribute__((always_inline)) {
-    if (SILU) {
-      const int o = min(out0 + (lr & (kQRows / 2 - 1)), N - 1);
-      return lr < kQRows / 2 ? o : N + o;
-    }
-    return min(out0 + lr, N - 1);
-  };
-
-  // First batch of weight loads, then x into LDS.
-  QRaw raw[kQBatch];
-  auto issue = [&](int p0) __attribute__((always_inline)) {
-#pragma unroll
-    for (int b = 0; b < kQBatch; ++b) {
-      int p = p0 + b * kQThreads;
-      p = p < total ? p : total - 1;  // clamped; the consumer skips it
-      raw[b] = qload<FMT>(W, L, row_of(p / P), p % P, K);
-    }
-  };
-  issue(tid);
-  __builtin_amdgcn_sched_barrier(0);
-  for (int i = tid * 8; i < K; i += kQThreads * 8)
-    *reinterpret_cast<u32x4*>(s_x + i) = load16(x + i);
-  __syncthreads();
-
-  for (int p0 = tid;; p0 += kQBatch * kQThreads) {
-#pragma unroll
-    for (int b = 0; b < kQBatch; ++b) {
-      const int p = p0 + b * kQThreads;
-      if (p < total) s_part[p] = qpiece<FMT>(raw[b], W, L, row_of(p / P), p % P, K, s_x);
-    }
-    if (p0 + kQBatch * kQThreads >= total) break;
-    issue(p0 + kQBatch * kQThreads);
-  }
-  __syncthreads();
-
-  // Row sums in a fixed order: 16 threads per row, each a strided partial,
-  // then a butterfly over the 16.
-  const int lr = tid >> 4, sub = tid & 15;
-  float s = 0.f;
-  for (int q = sub; q < P; q += 16) s += s_part[lr * P + q];
-#pragma unroll
-  for (int off = 8; off >= 1; off >>= 1) s += __shfl_xor(s, off, 16);
-  if (SILU) {
-    // lanes of gate row lr (< 8) and its up row lr + 8 sit 128 threads apart:
-    // pass the up sums through LDS
-    __syncthreads();
-    if (sub == 0 && lr >= kQRows / 2) s_part[lr - kQRows / 2] = s;
-    __syncthreads();
-    if (sub == 0 && lr < kQRows / 2 && out0 + lr < N) {
-      const half_t g = (half_t)s, u = (half_t)s_part[lr];
-      const float gf = (float)g;
-      const float sig = 1.0f / (1.0f + expf(-gf));
-      y[out0 + lr] = (half_t)(sig * gf * (float)u);
-    }
-  } else if (sub == 0 && out0 + lr < N) {
-    y[out0 + lr] = (half_t)s;
-  }
-}
-
-// ---------------------------------------------------------------- dequant to f16
 
 // f16 of p rounded to nearest even, with p's sign.  Rounding keeps the sign,
 // so the OR changes nothing in exact arithmetic; it is there because the
@@ -410,9 +610,7 @@ static bool qfmt_ok(int fmt, int N, int K) {
   if (N < 1 || K < 1) return false;
   const int blk = fmt == 8 ? 32 : 256;
   if (fmt != 8 && fmt != 12 && fmt != 14) return false;
-  if (K % blk != 0 || K > kQMaxK) return false;
-  const int P = K / (fmt == 8 ? 16 : 32);
-  return (long)kQRows * P <= kQMaxPieces;
+  return K % blk == 0 && K <= kQMaxK;
 }
 
 size_t qweight_bytes(int fmt, int N, int K) {
@@ -431,17 +629,80 @@ hipError_t launch_qweight_repack(int fmt, const void* src, int N, int K, void* d
   return hipGetLastError();
 }
 
+// Pieces per lane and slice with an instantiated kernel: 16-row workgroups
+// (S = 1) and 4-row workgroups (S = 1, 2, 4).
+static bool npw_tall(int v) { return v == 5 || v == 8 || v == 10 || v == 16 || v == 19; }
+static bool npw_short(int v) {
+  return v == 2 || v == 3 || v == 4 || v == 5 || v == 8 || v == 10 || v == 13;
+}
+
+template <int FMT, bool SILU, int R, int S>
+static void gemv_q_go(int npw, unsigned grid, size_t lds, const void* W, const void* x, void* y,
+                      int N, int K, const QLayout& L, hipStream_t stream) {
+  const uint8_t* w = (const uint8_t*)W;
+  const half_t* xi = (const half_t*)x;
+  half_t* yo = (half_t*)y;
+  constexpr int T = R * S * kQTeam;
+#define GROUT_QGO(V) \
+  case V: gemv_q_kernel<FMT, SILU, R, S, V><<<grid, T, lds, stream>>>(w, xi, yo, N, K, L); break;
+  if constexpr (R == 16) {
+    switch (npw) {
+      GROUT_QGO(5) GROUT_QGO(8) GROUT_QGO(10) GROUT_QGO(16) GROUT_QGO(19)
+      default: gemv_q_kernel<FMT, SILU, R, 1, 0><<<grid, T, lds, stream>>>(w, xi, yo, N, K, L);
+    }
+  } else if constexpr (SILU || S == 0) {
+    gemv_q_kernel<FMT, SILU, R, 1, 0><<<grid, R * kQTeam, lds, stream>>>(w, xi, yo, N, K, L);
+  } else {
+    switch (npw) {
+      GROUT_QGO(2) GROUT_QGO(3) GROUT_QGO(4) GROUT_QGO(5) GROUT_QGO(8) GROUT_QGO(10)
+      GROUT_QGO(13)
+      default: break;
+    }
+  }
+#undef GROUT_QGO
+}
+
+// LDS bytes of a workgroup of R rows in S slices (layout in gemv_q_kernel).
+template <int FMT>
+static size_t gemv_q_lds(int R, int S, int K) {
+  return (size_t)((K + 127) & ~127) * 2 + (size_t)(FMT == 8 ? K / 32 : K / 16) * 4 +
+         (size_t)R * (FMT == 8 ? K / 32 : K / 16) * 4 + (size_t)R * S * 4;
+}
+
 template <int FMT>
 static void gemv_q_launch(const void* W, const void* x, void* y, int N, int K, bool silu,
                           hipStream_t stream) {
-  const QLayout L = qlayout(FMT, (size_t)(silu ? 2 * N : N), (size_t)K);
-  const size_t lds = (size_t)K * 2 + (size_t)kQRows * (K / (FMT == 8 ? 16 : 32)) * 4;
-  if (silu)
-    gemv_q_kernel<FMT, true><<<(unsigned)((N + kQRows / 2 - 1) / (kQRows / 2)), kQThreads, lds,
-                                stream>>>((const uint8_t*)W, (const half_t*)x, (half_t*)y, N, K, L);
-  else
-    gemv_q_kernel<FMT, false><<<(unsigned)((N + kQRows - 1) / kQRows), kQThreads, lds, stream>>>(
-        (const uint8_t*)W, (const half_t*)x, (half_t*)y, N, K, L);
+  const int rows = silu ? 2 * N : N;
+  const QLayout L = qlayout(FMT, (size_t)rows, (size_t)K);
+  const int np = K % 512 == 0 ? K / 512 : 0;  // pieces per lane of a whole row
+  if (rows >= 16 * 1024 && gemv_q_lds<FMT>(16, 1, K) <= 65536) {
+    // tall: 16 rows per workgroup (x staged once per 16 rows)
+    const int per = silu ? 8 : 16;
+    const unsigned grid = (unsigned)((N + per - 1) / per);
+    const int npw = npw_tall(np) ? np : 0;
+    if (silu) gemv_q_go<FMT, true, 16, 1>(npw, grid, gemv_q_lds<FMT>(16, 1, K), W, x, y, N, K, L, stream);
+    else gemv_q_go<FMT, false, 16, 1>(npw, grid, gemv_q_lds<FMT>(16, 1, K), W, x, y, N, K, L, stream);
+    return;
+  }
+  // short: 4 rows per workgroup, each row split over S waves so that the grid
+  // holds about 2048 waves or more
+  const int per = silu ? 2 : 4;
+  const unsigned grid = (unsigned)((N + per - 1) / per);
+  if (silu) {
+    gemv_q_go<FMT, true, 4, 0>(0, grid, gemv_q_lds<FMT>(4, 1, K), W, x, y, N, K, L, stream);
+    return;
+  }
+  int S = 0, npw = 0;
+  if (np > 0) {
+    for (int s = grid >= 2048 ? 1 : grid >= 1024 ? 2 : 4; s <= 4 && S == 0; s *= 2) {
+      const int v = (np + s - 1) / s;
+      if (v <= np && npw_short(v)) S = s, npw = v;
+    }
+  }
+  if (S == 0) gemv_q_go<FMT, false, 4, 0>(0, grid, gemv_q_lds<FMT>(4, 1, K), W, x, y, N, K, L, stream);
+  else if (S == 1) gemv_q_go<FMT, false, 4, 1>(npw, grid, gemv_q_lds<FMT>(4, 1, K), W, x, y, N, K, L, stream);
+  else if (S == 2) gemv_q_go<FMT, false, 4, 2>(npw, grid, gemv_q_lds<FMT>(4, 2, K), W, x, y, N, K, L, stream);
+  else gemv_q_go<FMT, false, 4, 4>(npw, grid, gemv_q_lds<FMT>(4, 4, K), W, x, y, N, K, L, stream);
 }
 
 hipError_t launch_gemv_q(int fmt, const void* W, const void* x, void* y, int N, int K, bool silu,

@@ -72,7 +72,10 @@ FMTS = [(O.Q8_0, "Q8_0"), (O.Q4_K, "Q4_K"), (O.Q6_K, "Q6_K")]
 
 
 @pytest.mark.parametrize("fmt,name", FMTS)
-@pytest.mark.parametrize("n,k", [(6144, 2560), (2560, 9728), (2560, 4096), (37, 256), (1, 512)])
+# 4-row workgroups with 5 / 19 / 8 pieces per lane and the any-K path; 16-row
+# workgroups (>= 16384 rows) with a ragged last workgroup, exact and any-K
+@pytest.mark.parametrize("n,k", [(6144, 2560), (2560, 9728), (2560, 4096), (37, 256), (1, 512),
+                                 (16400, 2560), (16391, 768)])
 def test_gemv_q_vs_oracle(gpu, fmt, name, n, k):
     L = gpu.lib()
     print(f"gemv_q {name} n={n} k={k}", flush=True)
@@ -95,9 +98,9 @@ def test_gemv_q_vs_oracle(gpu, fmt, name, n, k):
 
 
 @pytest.mark.parametrize("fmt,name", FMTS)
-def test_gemv_q_silu_pairs_vs_oracle(gpu, fmt, name):
+@pytest.mark.parametrize("inter,k", [(1000, 2560), (8203, 2560), (9, 1280)])
+def test_gemv_q_silu_pairs_vs_oracle(gpu, fmt, name, inter, k):
     L = gpu.lib()
-    inter, k = 1000, 2560
     print(f"gemv_q_silu {name} inter={inter} k={k}", flush=True)
     # scales small enough that gate / up stay well inside the f16 range
     blocks = random_blocks(fmt, 2 * inter, k, seed=77 + fmt, dmax=4e-4)
