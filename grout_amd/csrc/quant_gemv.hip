@@ -116,6 +116,16 @@ constexpr int kQTeam = 16;  // lanes per weight row
 
 __device__ __forceinline__ float h2f_bits(uint16_t b) { return (float)__builtin_bit_cast(half_t, b); }
 
+// f16 of p rounded to nearest even, with p's sign.  Rounding keeps the sign,
+// so the OR changes nothing in exact arithmetic; it is there because the
+// compiler folds a product followed by this rounding into a mixed-precision
+// fma with a +0 addend, which turns a -0 product into +0.
+__device__ __forceinline__ half_t f2h_signed(float p) {
+  const uint16_t h = __builtin_bit_cast(uint16_t, (half_t)p);
+  return __builtin_bit_cast(half_t,
+                            (uint16_t)(h | ((__builtin_bit_cast(uint32_t, p) >> 16) & 0x8000u)));
+}
+
 // LDS granule (8 halves of x) for logical granule G.  Lane m of a team reads
 // granules whose bits 1-5 are functions of m; the map moves the lane-varying
 // bits onto bits 0-3 so any 8 or 16 lanes of a team hit distinct bank
@@ -333,8 +343,9 @@ __device__ __forceinline__ SRaw stage_load(const uint8_t* __restrict__ W, const 
   return s;
 }
 
-// Scales in fp32 as the reference forms them (d * sc, dmin * m), then times
-// the power of two that undoes the denormal encoding (exact).
+// Scales as the reference's decode layout holds them (Q8_0 d; Q6_K d * sc in
+// fp32; Q4_K the effective f16(d * sc) and f16(dmin * m)), times the power of
+// two that undoes the denormal encoding (exact).
 template <int FMT>
 __device__ __forceinline__ void stage_store(const SRaw& s, int u, int U, int UPR, int SCW,
                                             float* s_sc) {
@@ -364,8 +375,10 @@ __device__ __forceinline__ void stage_store(const SRaw& s, int u, int U, int UPR
 #pragma unroll
     for (int g = 0; g < 4; ++g)
       *reinterpret_cast<floatx4*>(dst + 16 * k + 4 * g) =
-          floatx4{(d * (float)sc[2 * g]) * 0x1p24f, dmin * (float)mn[2 * g],
-                  (d * (float)sc[2 * g + 1]) * 0x1p20f, dmin * (float)mn[2 * g + 1]};
+          floatx4{(float)f2h_signed(d * (float)sc[2 * g]) * 0x1p24f,
+                  (float)f2h_signed(dmin * (float)mn[2 * g]),
+                  (float)f2h_signed(d * (float)sc[2 * g + 1]) * 0x1p20f,
+                  (float)f2h_signed(dmin * (float)mn[2 * g + 1])};
   } else {
     const float d = h2f_bits((uint16_t)s.d);
     float f[16];
@@ -531,15 +544,6 @@ __device__ __forceinline__ QRaw qload(const uint8_t* __restrict__ W, const QLayo
 }
 
 
-// f16 of p rounded to nearest even, with p's sign.  Rounding keeps the sign,
-// so the OR changes nothing in exact arithmetic; it is there because the
-// compiler folds a product followed by this rounding into a mixed-precision
-// fma with a +0 addend, which turns a -0 product into +0.
-__device__ __forceinline__ half_t f2h_signed(float p) {
-  const uint16_t h = __builtin_bit_cast(uint16_t, (half_t)p);
-  return __builtin_bit_cast(half_t,
-                            (uint16_t)(h | ((__builtin_bit_cast(uint32_t, p) >> 16) & 0x8000u)));
-}
 
 // w[row][k] as f16 (for the prefill GEMMs): one thread per 16-byte piece.
 template <int FMT>
@@ -576,8 +580,9 @@ __global__ __launch_bounds__(256) void qdequant_kernel(const uint8_t* __restrict
         m[t] = (sc[jj + 4] >> 4) | ((sc[jj] >> 6) << 4);
       }
     }
-    const float d1 = d * (float)s[0], m1 = dmin * (float)m[0];
-    const float d2 = d * (float)s[1], m2 = dmin * (float)m[1];
+    // effective scales of the decode layout: f16(d * sc), f16(dmin * m)
+    const float d1 = (float)f2h_signed(d * (float)s[0]), m1 = (float)f2h_signed(dmin * (float)m[0]);
+    const float d2 = (float)f2h_signed(d * (float)s[1]), m2 = (float)f2h_signed(dmin * (float)m[1]);
     const uint8_t* q = reinterpret_cast<const uint8_t*>(&r.a);
     const int e0 = sb * 256 + 64 * g + l0;
     for (int i = 0; i < 16; ++i) {

@@ -21,16 +21,27 @@
  *         i=2: ql[64n+l] high,   qh bits 4-5,        sc[8n + l/16 + 4]
  *         i=3: ql[64n+l+32] high,qh bits 6-7,        sc[8n + l/16 + 6]
  *                                                          w = d*sc*(q - 32)
- * Every product is fp32 in the order the reference writes it.  The GEMV
- * reference is y[n] = sum_k w[n][k] * x[k] accumulated in fp64 here (the
- * reference accumulates in fp32, src/kernels.rs:259-428), so the GPU result
- * differs from this only by fp32 rounding.
+ * Every product is fp32 in the order the reference writes it.
+ *
+ * Decode layout (decode != 0): the reference's GPU decode path repacks Q4_K
+ * with the per-32 effective scale and min folded and rounded to f16,
+ * sc = f16(d * sc6), mn = f16(dmin * m6) (repack_q4k_soa_host,
+ * src/loader.rs:437-486), and both its decode GEMV (gemv_q4k_soa_f16,
+ * src/kernels.rs:709-803) and its prefill dequant (dequant_q4k_soa_to_f16,
+ * src/kernels.rs:1113-1160) compute w = sc * q - mn from those.  Its Q8_0
+ * and Q6_K decode layouts keep d and sc as stored, so the two modes agree
+ * for them.
+ *
+ * The GEMV reference is y[n] = sum_k w[n][k] * x[k] over the decode-layout
+ * weights, accumulated in fp64 here (the reference accumulates in fp32), so
+ * the GPU result differs from this only by fp32 rounding.
  */
 #include <stddef.h>
 #include <stdint.h>
 #include <string.h>
 
 float go_h2f(uint16_t h);
+uint16_t go_f2h(float f);
 
 enum { GQ_Q8_0 = 8, GQ_Q4_K = 12, GQ_Q6_K = 14 };
 
@@ -52,8 +63,11 @@ int go_qblock_bytes(int fmt) {
 }
 int go_qblock_elems(int fmt) { return fmt == GQ_Q8_0 ? 32 : 256; }
 
-/* Dequantizes n weights (a multiple of the block size) into fp32. */
-int go_dequant(int fmt, const uint8_t* blocks, size_t n, float* out) {
+static float round_f16(float f) { return go_h2f(go_f2h(f)); }
+
+/* Dequantizes n weights (a multiple of the block size) into fp32; decode
+ * selects the decode-layout Q4_K scales. */
+static int dequant_mode(int fmt, const uint8_t* blocks, size_t n, float* out, int decode) {
   const int be = go_qblock_elems(fmt), bb = go_qblock_bytes(fmt);
   if (bb < 0 || n % (size_t)be) return -1;
   for (size_t b = 0; b < n / (size_t)be; ++b) {
@@ -69,9 +83,15 @@ int go_dequant(int fmt, const uint8_t* blocks, size_t n, float* out) {
       for (int g = 0; g < 4; ++g) {
         int sc, m;
         scale_min_k4(2 * g, scales, &sc, &m);
-        const float d1 = d * (float)sc, m1 = dmin * (float)m;
+        float d1 = d * (float)sc, m1 = dmin * (float)m;
         scale_min_k4(2 * g + 1, scales, &sc, &m);
-        const float d2 = d * (float)sc, m2 = dmin * (float)m;
+        float d2 = d * (float)sc, m2 = dmin * (float)m;
+        if (decode) { /* src/loader.rs:458-461 */
+          d1 = round_f16(d1);
+          m1 = round_f16(m1);
+          d2 = round_f16(d2);
+          m2 = round_f16(m2);
+        }
         for (int l = 0; l < 32; ++l) {
           y[64 * g + l] = d1 * (float)(qs[32 * g + l] & 0xF) - m1;
           y[64 * g + 32 + l] = d2 * (float)(qs[32 * g + l] >> 4) - m2;
@@ -102,8 +122,18 @@ int go_dequant(int fmt, const uint8_t* blocks, size_t n, float* out) {
   return 0;
 }
 
-/* y[r] = sum_k w[r][k] * x[k] (fp64) for rows of K weights stored as ggml
- * blocks, rows contiguous. */
+/* CPU dequantization rule (src/dequant.rs:211-323). */
+int go_dequant(int fmt, const uint8_t* blocks, size_t n, float* out) {
+  return dequant_mode(fmt, blocks, n, out, 0);
+}
+
+/* Decode-layout dequantization (Q4_K with f16 effective scales). */
+int go_dequant_decode(int fmt, const uint8_t* blocks, size_t n, float* out) {
+  return dequant_mode(fmt, blocks, n, out, 1);
+}
+
+/* y[r] = sum_k w[r][k] * x[k] (fp64) over the decode-layout weights of rows
+ * of K weights stored as ggml blocks, rows contiguous. */
 int go_gemv_q(int fmt, const uint8_t* blocks, int N, int K, const uint16_t* x, double* y) {
   const int be = go_qblock_elems(fmt), bb = go_qblock_bytes(fmt);
   if (bb < 0 || K % be) return -1;
@@ -111,7 +141,7 @@ int go_gemv_q(int fmt, const uint8_t* blocks, int N, int K, const uint16_t* x, d
   if (K > 16384) return -1;
   const size_t row_bytes = (size_t)(K / be) * (size_t)bb;
   for (int r = 0; r < N; ++r) {
-    go_dequant(fmt, blocks + (size_t)r * row_bytes, (size_t)K, row);
+    dequant_mode(fmt, blocks + (size_t)r * row_bytes, (size_t)K, row, 1);
     double s = 0.0;
     for (int k = 0; k < K; ++k) s += (double)row[k] * (double)go_h2f(x[k]);
     y[r] = s;

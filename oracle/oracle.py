@@ -73,6 +73,7 @@ _SIGS = {
     "go_qblock_bytes": (_i, [_i]),
     "go_qblock_elems": (_i, [_i]),
     "go_dequant": (_i, [_i, _u8p, _sz, _f32p]),
+    "go_dequant_decode": (_i, [_i, _u8p, _sz, _f32p]),
     "go_gemv_q": (_i, [_i, _u8p, _i, _i, _u16p, _f64p]),
 }
 
@@ -225,17 +226,22 @@ def qblock(fmt: int):
     return int(lib().go_qblock_elems(fmt)), int(lib().go_qblock_bytes(fmt))
 
 
-def dequant(fmt: int, blocks, n: int) -> np.ndarray:
-    """ggml blocks (uint8) -> n fp32 weights (src/dequant.rs:211-323)."""
+def dequant(fmt: int, blocks, n: int, decode: bool = False) -> np.ndarray:
+    """ggml blocks (uint8) -> n fp32 weights: the CPU rule
+    (src/dequant.rs:211-323), or with decode=True the reference's GPU decode
+    layout, whose Q4_K scale and min are folded and rounded to f16
+    (src/loader.rs:437-486)."""
     out = np.empty(n, np.float32)
-    rc = lib().go_dequant(fmt, np.ascontiguousarray(blocks, np.uint8).reshape(-1), n, out)
+    fn = lib().go_dequant_decode if decode else lib().go_dequant
+    rc = fn(fmt, np.ascontiguousarray(blocks, np.uint8).reshape(-1), n, out)
     if rc != 0:
         raise ValueError(f"dequant of format {fmt} with {n} weights failed")
     return out
 
 
 def gemv_q(fmt: int, blocks, N: int, K: int, x) -> np.ndarray:
-    """y = W x in fp64 for rows of ggml blocks (the quantized GEMV reference)."""
+    """y = W x in fp64 for rows of ggml blocks, W the decode-layout weights
+    (the reference's decode GEMVs, src/kernels.rs:565-803)."""
     y = np.empty(N, np.float64)
     rc = lib().go_gemv_q(fmt, np.ascontiguousarray(blocks, np.uint8).reshape(-1), N, K, _u16(x), y)
     if rc != 0:

@@ -2,13 +2,14 @@
 dequantization oracle, through the C ABI.
 
 Inputs: random ggml blocks (random payload bytes, scales/mins, d and dmin
-drawn as f16 in [1e-3, 2e-2]).  Bars: the repacked weights dequantize
-bit-exactly (the kernel's fp32 dequantization rounded once to f16 equals the
-oracle's); GEMV outputs within one f16 ulp plus 1e-5 x sum(|w x| + m |x|) of
-the fp64 oracle (fp32 accumulation in another order; for Q4_K the scale and
-min are factored out of each 16-weight run, so the min term enters the
-bound); the SiLU-pair epilogue within the bound propagated through
-silu(g) * u plus one ulp."""
+drawn as f16 in [1e-3, 2e-2]).  The oracle runs in its decode-layout mode
+(Q4_K effective scale and min rounded to f16, as the reference's decode
+repack holds them).  Bars: the repacked weights dequantize bit-exactly (the
+kernel's fp32 dequantization rounded once to f16 equals the oracle's); GEMV
+outputs within one f16 ulp plus 1e-5 x sum(|w x| + m |x|) of the fp64 oracle
+(fp32 accumulation in another order; for Q4_K the scale and min are factored
+out of each 16-weight run, so the min term enters the bound); the SiLU-pair
+epilogue within the bound propagated through silu(g) * u plus one ulp."""
 import ctypes as C
 
 import numpy as np
@@ -128,7 +129,8 @@ def test_gemv_q_silu_pairs_vs_oracle(gpu, fmt, name, inter, k):
 
 @pytest.mark.parametrize("fmt,name", FMTS)
 def test_qweight_dequant_bit_exact(gpu, fmt, name):
-    """The GPU's fp32 dequantization rounded to f16 equals the oracle's."""
+    """The GPU's dequantization (decode-layout scales, fp32 arithmetic, one
+    rounding to f16) equals the oracle's bit for bit."""
     L = gpu.lib()
     n, k = 48, 1024
     blocks = random_blocks(fmt, n, k, seed=3 + fmt)
@@ -136,7 +138,7 @@ def test_qweight_dequant_bit_exact(gpu, fmt, name):
     out = torch.empty((n, k), dtype=torch.float16, device="cuda")
     call(L, "grout_qweight_dequant", fmt, ptr(wq), n, k, ptr(out), None)
     torch.cuda.synchronize()
-    want = O.dequant(fmt, blocks, n * k).reshape(n, k).astype(np.float16)
+    want = O.dequant(fmt, blocks, n * k, decode=True).reshape(n, k).astype(np.float16)
     got = out.cpu().numpy()
     bad = np.argwhere(got.view(np.uint16) != want.view(np.uint16))
     if len(bad):

@@ -1,4 +1,5 @@
-"""CPU pins of the ggml dequantization oracle (oracle/ggml_quant.c).
+"""CPU pins of the ggml dequantization oracle (oracle/ggml_quant.c), in both
+its CPU-rule and decode-layout modes.
 
 Each format is checked against blocks built by an independent *encoder*
 written here from the published block layout (the inverse of the decode: a
@@ -95,6 +96,30 @@ def test_q4_k_against_encoder(seed):
     assert np.array_equal(got, want.astype(f32))
 
 
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_q4_k_decode_layout_against_encoder(seed):
+    """Decode layout: effective scale f16(d * sc) and min f16(dmin * m)."""
+    rng = np.random.default_rng(20 + seed)
+    d, dmin = F16(rng.uniform(1e-3, 0.1)), F16(rng.uniform(1e-3, 0.1))
+    sc, m = rng.integers(0, 64, 8), rng.integers(0, 64, 8)
+    sc[5], m[6] = 63, 63
+    q = rng.integers(0, 16, 256)
+    blk = enc_q4_k(d, dmin, sc, m, q)
+    got = O.dequant(O.Q4_K, blk, 256, decode=True)
+    f32 = np.float32
+    s_eff = (f32(d) * sc.astype(f32)).astype(F16).astype(f32)
+    m_eff = (f32(dmin) * m.astype(f32)).astype(F16).astype(f32)
+    want = np.repeat(s_eff, 32) * q.astype(f32) - np.repeat(m_eff, 32)
+    assert np.array_equal(got, want.astype(f32))
+    # the rounding is visible: the CPU rule differs somewhere in the block
+    assert not np.array_equal(got, O.dequant(O.Q4_K, blk, 256))
+    # Q8_0 and Q6_K: both modes agree
+    b8 = enc_q8_0(0.37, rng.integers(-128, 128, 32))
+    assert np.array_equal(O.dequant(O.Q8_0, b8, 32, decode=True), O.dequant(O.Q8_0, b8, 32))
+    b6 = enc_q6_k(F16(0.0123), rng.integers(-128, 128, 16), rng.integers(0, 64, 256))
+    assert np.array_equal(O.dequant(O.Q6_K, b6, 256, decode=True), O.dequant(O.Q6_K, b6, 256))
+
+
 @pytest.mark.parametrize("seed", [0, 1])
 def test_q6_k_against_encoder(seed):
     rng = np.random.default_rng(10 + seed)
@@ -117,7 +142,7 @@ def test_gemv_q_is_dequant_times_x():
                             for _ in range(K // 256)]) for _ in range(N)]
     blocks = np.stack(rows)
     x = rng.standard_normal(K).astype(F16).view(np.uint16)
-    w = O.dequant(O.Q4_K, blocks, N * K).reshape(N, K).astype(np.float64)
+    w = O.dequant(O.Q4_K, blocks, N * K, decode=True).reshape(N, K).astype(np.float64)
     want = w @ O.h2f(x).astype(np.float64)
     assert np.allclose(O.gemv_q(O.Q4_K, blocks, N, K, x), want, rtol=0, atol=1e-12)
 
