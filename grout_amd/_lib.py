@@ -48,6 +48,22 @@ class Qwen3Weights(C.Structure):
                 ("layers", C.POINTER(Qwen3Layer))]
 
 
+class WPart(C.Structure):
+    _fields_ = [("fmt", _i), ("rows", _i), ("data", _p)]
+
+
+class Qwen3QLayer(C.Structure):
+    _fields_ = [("input_layernorm", _p), ("num_qkv_parts", _i), ("qkv", WPart * 3),
+                ("q_norm", _p), ("k_norm", _p), ("o_proj", WPart),
+                ("post_attention_layernorm", _p), ("num_gate_up_parts", _i),
+                ("gate_up", WPart * 2), ("down_proj", WPart)]
+
+
+class Qwen3QWeights(C.Structure):
+    _fields_ = [("embed_tokens", WPart), ("norm", _p), ("lm_head", WPart),
+                ("layers", C.POINTER(Qwen3QLayer))]
+
+
 class ModelInfo(C.Structure):
     _fields_ = [("config", Qwen3Config), ("tie_word_embeddings", _i), ("num_eos", _i),
                 ("eos_token_ids", _u32 * 8), ("weight_bytes", _sz)]
@@ -90,10 +106,13 @@ SIGNATURES = {
     "grout_gemv_q": (_i, [_i, _p, _p, _p, _i, _i, _p]),
     "grout_gemv_q_silu_mul": (_i, [_i, _p, _p, _p, _i, _i, _p]),
     "grout_qweight_dequant": (_i, [_i, _p, _i, _i, _p, _p]),
+    "grout_qweight_gather": (_i, [_i, _p, _i, _i, _p, _i, _p, _p]),
     "grout_argmax_workspace_bytes": (_sz, [_i]),
     "grout_argmax": (_i, [_p, _i, _p, _sz, _p, _p]),
     "grout_engine_create": (_i, [C.POINTER(Qwen3Config), C.POINTER(Qwen3Weights), _i,
                                  C.POINTER(_p)]),
+    "grout_engine_create_q": (_i, [C.POINTER(Qwen3Config), C.POINTER(Qwen3QWeights), _i,
+                                   C.POINTER(_p)]),
     "grout_model_inspect": (_i, [C.c_char_p, C.POINTER(ModelInfo)]),
     "grout_model_load": (_i, [C.c_char_p, _i, C.POINTER(_p)]),
     "grout_model_get_info": (_i, [_p, C.POINTER(ModelInfo)]),

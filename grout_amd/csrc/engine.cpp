@@ -19,6 +19,7 @@
 #include <hip/hip_runtime.h>
 #include <rocblas/rocblas.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <new>
@@ -53,10 +54,34 @@ struct Arena {
   }
 };
 
+// One weight matrix (a part of a projection): f16 [rows][k] or a low-bit
+// layout (grout_qweight_repack).
+struct Mat {
+  int fmt = GROUT_WFMT_F16;
+  int rows = 0;
+  const void* data = nullptr;
+};
+
+struct LayerW {
+  const void* input_norm = nullptr;
+  const void* q_norm = nullptr;
+  const void* k_norm = nullptr;
+  const void* post_norm = nullptr;
+  int nqkv = 0;
+  Mat qkv[3];  // q | k | v rows
+  Mat o;
+  int ngu = 0;
+  Mat gu[2];  // gate | up rows
+  Mat down;
+};
+
+// A projection held as one f16 matrix: the fused-norm f16 GEMV paths apply.
+bool single_f16(const Mat* parts, int n) { return n == 1 && parts[0].fmt == GROUT_WFMT_F16; }
+
 // Decode-step activations: one token.
 struct DecodeBufs {
-  size_t hidden, normed, hidden_after_attn, qkv, attn_out, attn_proj, ff, ff_down, logits,
-      argmax_max, argmax_idx, token, pos, workspace;
+  size_t hidden, normed, hidden_after_attn, qkv, attn_out, attn_proj, gate_up, ff, ff_down,
+      logits, argmax_max, argmax_idx, token, pos, workspace;
 };
 
 // Prefill activations: cap rows.
@@ -80,10 +105,10 @@ int blas_status(rocblas_status s, const char* what) {
 
 struct grout_engine {
   grout_qwen3_config cfg{};
-  const void* embed = nullptr;
+  Mat embed;
   const void* final_norm = nullptr;
-  const void* lm_head = nullptr;
-  std::vector<grout_qwen3_layer> layers;
+  Mat lm_head;
+  std::vector<LayerW> layers;
   int device = 0;
   hipStream_t stream = nullptr;
   rocblas_handle blas = nullptr;
@@ -104,6 +129,9 @@ struct grout_engine {
   Arena pre;
   PrefillBufs pb{};
   int prefill_cap = 0;
+  // f16 copy of one low-bit matrix at a time for the prefill GEMMs
+  void* deq = nullptr;
+  size_t deq_bytes = 0;
 
   // Pinned host staging.
   uint16_t* h_logits = nullptr;
@@ -140,23 +168,68 @@ struct grout_engine {
 
 namespace {
 
-// y[rows][n] = x[rows][k] . W[n][k]^T, fp16 in/out, fp32 accumulation.  In
-// rocBLAS's column-major terms: C (n x rows, ldc n) = W^T(col-major k x n,
-// transposed) x X (col-major k x rows).
-int gemm_rows(grout_engine* e, const void* W, const void* x, void* y, int rows, int n, int k) {
+// y[rows][0..n) = x[rows][k] . W[n][k]^T with y's rows ldy apart, fp16
+// in/out, fp32 accumulation.  In rocBLAS's column-major terms: C (n x rows,
+// ldc ldy) = W^T (col-major k x n, transposed) x X (col-major k x rows).
+int gemm_rows(grout_engine* e, const void* W, const void* x, void* y, int rows, int n, int k,
+              int ldy) {
   const float alpha = 1.f, beta = 0.f;
   return blas_status(
       rocblas_gemm_ex(e->blas, rocblas_operation_transpose, rocblas_operation_none, n, rows, k,
                       &alpha, W, rocblas_datatype_f16_r, k, x, rocblas_datatype_f16_r, k, &beta, y,
-                      rocblas_datatype_f16_r, n, y, rocblas_datatype_f16_r, n,
+                      rocblas_datatype_f16_r, ldy, y, rocblas_datatype_f16_r, ldy,
                       rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0),
       "rocblas_gemm_ex");
 }
 
-// Projection of `rows` tokens.  One row uses the decode GEMV kernel.
+// Projection of `rows` tokens by an f16 matrix.  One row uses the decode
+// GEMV kernel.
 int project(grout_engine* e, const void* W, const void* x, void* y, int rows, int n, int k) {
   if (rows == 1) return hip_status(grout::launch_gemv(W, x, y, n, k, e->stream), "gemv");
-  return gemm_rows(e, W, x, y, rows, n, k);
+  return gemm_rows(e, W, x, y, rows, n, k, n);
+}
+
+// One token through one weight part with the decode GEMV of its format.
+int mat_gemv(grout_engine* e, const Mat& m, const void* x, void* y, int k) {
+  if (m.fmt == GROUT_WFMT_F16)
+    return hip_status(grout::launch_gemv(m.data, x, y, m.rows, k, e->stream), "gemv");
+  return hip_status(grout::launch_gemv_q(m.fmt, m.data, x, y, m.rows, k, false, e->stream),
+                    "gemv_q");
+}
+
+// f16 [rows][k] form of a part for the prefill GEMM: an f16 part as it is, a
+// low-bit part dequantized into the engine's scratch (the scratch holds one
+// matrix at a time; stream order keeps its reuse safe).
+int mat_f16(grout_engine* e, const Mat& m, int k, const void** w) {
+  if (m.fmt == GROUT_WFMT_F16) {
+    *w = m.data;
+    return GROUT_OK;
+  }
+  GROUT_CHECK(hip_status(grout::launch_qweight_dequant(m.fmt, m.data, m.rows, k, e->deq, e->stream),
+                         "qweight dequant"));
+  *w = e->deq;
+  return GROUT_OK;
+}
+
+// Projection of `rows` tokens by one part into columns [0, m.rows) of y
+// (rows ldy apart).
+int mat_project(grout_engine* e, const Mat& m, const void* x, void* y, int rows, int k, int ldy) {
+  if (m.fmt == GROUT_WFMT_F16 && ldy == m.rows) return project(e, m.data, x, y, rows, m.rows, k);
+  const void* w = nullptr;
+  GROUT_CHECK(mat_f16(e, m, k, &w));
+  return gemm_rows(e, w, x, y, rows, m.rows, k, ldy);
+}
+
+// Token-embedding rows for ids (device memory).
+int embed_rows(grout_engine* e, const uint32_t* ids, void* out, int rows) {
+  const auto& c = e->cfg;
+  if (e->embed.fmt == GROUT_WFMT_F16)
+    return hip_status(grout::launch_embedding(ids, e->embed.data, out, rows, c.hidden_size,
+                                              c.vocab_size, e->stream),
+                      "embedding");
+  return hip_status(grout::launch_qgather(e->embed.fmt, e->embed.data, c.vocab_size, c.hidden_size,
+                                          ids, rows, out, e->stream),
+                    "embedding gather");
 }
 
 int norm(grout_engine* e, const void* residual, const void* x, const void* w, void* out,
@@ -172,58 +245,72 @@ int head(grout_engine* e, const void* hidden_after_attn, const void* ff_down) {
   const auto& c = e->cfg;
   GROUT_CHECK(norm(e, hidden_after_attn, ff_down, e->final_norm, e->d(e->db.normed),
                    e->d(e->db.hidden), 1));
-  GROUT_CHECK(hip_status(grout::launch_gemv(e->lm_head, e->d(e->db.normed), e->d(e->db.logits),
-                                            c.vocab_size, c.hidden_size, e->stream),
-                         "lm_head gemv"));
+  GROUT_CHECK(mat_gemv(e, e->lm_head, e->d(e->db.normed), e->d(e->db.logits), c.hidden_size));
   return hip_status(grout::launch_argmax(e->d(e->db.logits), e->d<float>(e->db.argmax_max),
                                          e->d<uint32_t>(e->db.argmax_idx), c.vocab_size,
                                          e->d<uint32_t>(e->db.token), e->stream),
                     "argmax");
 }
 
-// The decode step, as recorded into the graph.
+// The decode step, as recorded into the graph.  A projection held as one f16
+// matrix takes the fused norm + GEMV kernels; otherwise the norm runs on its
+// own and each part takes the GEMV of its format.
 int record_decode_step(grout_engine* e) {
   const auto& c = e->cfg;
   const DecodeBufs& b = e->db;
   hipStream_t s = e->stream;
-  GROUT_CHECK(hip_status(grout::launch_embedding(e->d<uint32_t>(b.token), e->embed,
-                                                 e->d(b.hidden), 1, c.hidden_size, c.vocab_size,
-                                                 s),
-                         "embedding"));
+  const int H = c.hidden_size, I = c.intermediate_size;
+  GROUT_CHECK(embed_rows(e, e->d<uint32_t>(b.token), e->d(b.hidden), 1));
   for (int l = 0; l < c.num_layers; ++l) {
-    const grout_qwen3_layer& w = e->layers[l];
-    // input norm fused into the QKV GEMV (layer 0: plain RMSNorm of the
-    // embedding; later layers: add the previous layer's MLP output first)
-    if (l == 0)
-      GROUT_CHECK(hip_status(grout::launch_gemv_norm(w.qkv_proj, nullptr, e->d(b.hidden),
-                                                     w.input_layernorm, nullptr, c.rms_norm_eps,
-                                                     e->d(b.qkv), e->qkv_dim, c.hidden_size,
-                                                     false, s),
+    const LayerW& w = e->layers[l];
+    // input norm (layer 0: plain RMSNorm of the embedding; later layers: add
+    // the previous layer's MLP output first), then the QKV projection
+    const void* res = l == 0 ? nullptr : e->d(b.hidden_after_attn);
+    const void* xin = l == 0 ? e->d(b.hidden) : e->d(b.ff_down);
+    void* res_out = l == 0 ? nullptr : e->d(b.hidden);
+    if (single_f16(w.qkv, w.nqkv)) {
+      GROUT_CHECK(hip_status(grout::launch_gemv_norm(w.qkv[0].data, res, xin, w.input_norm,
+                                                     res_out, c.rms_norm_eps, e->d(b.qkv),
+                                                     e->qkv_dim, H, false, s),
                              "qkv gemv"));
-    else
-      GROUT_CHECK(hip_status(grout::launch_gemv_norm(w.qkv_proj, e->d(b.hidden_after_attn),
-                                                     e->d(b.ff_down), w.input_layernorm,
-                                                     e->d(b.hidden), c.rms_norm_eps, e->d(b.qkv),
-                                                     e->qkv_dim, c.hidden_size, false, s),
-                             "qkv gemv"));
+    } else {
+      GROUT_CHECK(norm(e, res, xin, w.input_norm, e->d(b.normed), res_out, 1));
+      size_t row = 0;
+      for (int i = 0; i < w.nqkv; ++i) {
+        GROUT_CHECK(mat_gemv(e, w.qkv[i], e->d(b.normed), e->d<uint16_t>(b.qkv) + row, H));
+        row += (size_t)w.qkv[i].rows;
+      }
+    }
     // QK-norm/RoPE + K/V cache write inside the split-K attention, then the merge
     GROUT_CHECK(grout_attn_decode_fused(
         e->d(b.qkv), w.q_norm, w.k_norm, e->rope_cos(), e->rope_sin(), e->k_cache(l),
         e->v_cache(l), e->d(b.attn_out), e->d(b.workspace), e->ws_bytes,
         e->d<uint32_t>(b.pos), c.num_q_heads, c.num_kv_heads, 128, c.max_ctx, e->head_stride,
         e->num_splits, c.rms_norm_eps, e->qk_scale, s));
-    GROUT_CHECK(project(e, w.o_proj, e->d(b.attn_out), e->d(b.attn_proj), 1, c.hidden_size,
-                        e->q_dim));
-    // post-attention add + RMSNorm fused into the gate_up GEMV, whose
-    // epilogue applies SiLU(gate) * up: it writes ff directly
-    GROUT_CHECK(hip_status(grout::launch_gemv_norm(w.gate_up_proj, e->d(b.hidden),
-                                                   e->d(b.attn_proj), w.post_attention_layernorm,
-                                                   e->d(b.hidden_after_attn), c.rms_norm_eps,
-                                                   e->d(b.ff), c.intermediate_size,
-                                                   c.hidden_size, true, s),
-                           "gate_up gemv"));
-    GROUT_CHECK(project(e, w.down_proj, e->d(b.ff), e->d(b.ff_down), 1, c.hidden_size,
-                        c.intermediate_size));
+    GROUT_CHECK(mat_gemv(e, w.o, e->d(b.attn_out), e->d(b.attn_proj), e->q_dim));
+    // post-attention add + RMSNorm, gate_up and SiLU(gate) * up into ff
+    if (single_f16(w.gu, w.ngu)) {
+      GROUT_CHECK(hip_status(grout::launch_gemv_norm(w.gu[0].data, e->d(b.hidden),
+                                                     e->d(b.attn_proj), w.post_norm,
+                                                     e->d(b.hidden_after_attn), c.rms_norm_eps,
+                                                     e->d(b.ff), I, H, true, s),
+                             "gate_up gemv"));
+    } else {
+      GROUT_CHECK(norm(e, e->d(b.hidden), e->d(b.attn_proj), w.post_norm, e->d(b.normed),
+                       e->d(b.hidden_after_attn), 1));
+      if (w.ngu == 1) {
+        GROUT_CHECK(hip_status(grout::launch_gemv_q(w.gu[0].fmt, w.gu[0].data, e->d(b.normed),
+                                                    e->d(b.ff), I, H, true, s),
+                               "gate_up gemv_q"));
+      } else {
+        GROUT_CHECK(mat_gemv(e, w.gu[0], e->d(b.normed), e->d(b.gate_up), H));
+        GROUT_CHECK(mat_gemv(e, w.gu[1], e->d(b.normed), e->d<uint16_t>(b.gate_up) + w.gu[0].rows,
+                             H));
+        GROUT_CHECK(hip_status(grout::launch_silu_mul(e->d(b.gate_up), e->d(b.ff), 1, I, s),
+                               "silu_mul"));
+      }
+    }
+    GROUT_CHECK(mat_gemv(e, w.down, e->d(b.ff), e->d(b.ff_down), I));
   }
   return head(e, e->d(b.hidden_after_attn), e->d(b.ff_down));
 }
@@ -324,8 +411,8 @@ int decode_common(grout_engine* e, uint32_t token) {
   return GROUT_OK;
 }
 
-int validate(const grout_qwen3_config* c, const grout_qwen3_weights* w) {
-  GROUT_NEED(c != nullptr && w != nullptr, GROUT_EINVAL, "config or weights is NULL");
+int validate_config(const grout_qwen3_config* c) {
+  GROUT_NEED(c != nullptr, GROUT_EINVAL, "config is NULL");
   GROUT_NEED(c->num_layers >= 1, GROUT_EINVAL, "num_layers=%d", c->num_layers);
   GROUT_CHECK(check_heads(c->num_q_heads, c->num_kv_heads, c->head_dim, kMaxDecodeGroup));
   GROUT_NEED(c->hidden_size >= 8 && c->hidden_size % 8 == 0 && c->hidden_size <= 8192,
@@ -339,9 +426,20 @@ int validate(const grout_qwen3_config* c, const grout_qwen3_weights* w) {
              "rms_norm_eps=%g", (double)c->rms_norm_eps);
   GROUT_NEED(std::isfinite(c->rope_theta) && c->rope_theta > 0.f, GROUT_EINVAL, "rope_theta=%g",
              (double)c->rope_theta);
+  return GROUT_OK;
+}
+
+// The f16 API's weights as single-part projections.
+int convert_f16(const grout_qwen3_config* c, const grout_qwen3_weights* w, Mat& embed,
+                Mat& lm_head, std::vector<LayerW>& layers) {
+  GROUT_NEED(w != nullptr, GROUT_EINVAL, "weights is NULL");
   GROUT_CHECK(check_ptrs16({{w->embed_tokens, "embed_tokens"}, {w->norm, "norm"},
                             {w->lm_head, "lm_head"}}));
   GROUT_NEED(w->layers != nullptr, GROUT_EINVAL, "layers is NULL");
+  const int qd = c->num_q_heads * 128, qkv = qd + 2 * c->num_kv_heads * 128;
+  embed = Mat{GROUT_WFMT_F16, c->vocab_size, w->embed_tokens};
+  lm_head = Mat{GROUT_WFMT_F16, c->vocab_size, w->lm_head};
+  layers.assign(c->num_layers, LayerW{});
   for (int l = 0; l < c->num_layers; ++l) {
     const grout_qwen3_layer& L = w->layers[l];
     const int rc = check_ptrs16({{L.input_layernorm, "input_layernorm"},
@@ -353,18 +451,133 @@ int validate(const grout_qwen3_config* c, const grout_qwen3_weights* w) {
                                  {L.gate_up_proj, "gate_up_proj"},
                                  {L.down_proj, "down_proj"}});
     if (rc != GROUT_OK) return fail(rc, "layer %d: %s", l, g_last_error.c_str());
+    LayerW& o = layers[l];
+    o.input_norm = L.input_layernorm;
+    o.q_norm = L.q_norm;
+    o.k_norm = L.k_norm;
+    o.post_norm = L.post_attention_layernorm;
+    o.nqkv = 1;
+    o.qkv[0] = Mat{GROUT_WFMT_F16, qkv, L.qkv_proj};
+    o.o = Mat{GROUT_WFMT_F16, c->hidden_size, L.o_proj};
+    o.ngu = 1;
+    o.gu[0] = Mat{GROUT_WFMT_F16, 2 * c->intermediate_size, L.gate_up_proj};
+    o.down = Mat{GROUT_WFMT_F16, c->hidden_size, L.down_proj};
   }
   return GROUT_OK;
 }
 
-int create_impl(grout_engine* e, const grout_qwen3_config* c, const grout_qwen3_weights* w,
-                int device) {
+int check_part(const grout_wpart& p, int k, const char* what, int layer) {
+  const char* lname = layer < 0 ? "" : " of layer ";
+  GROUT_NEED(p.fmt == GROUT_WFMT_F16 || p.fmt == GROUT_WFMT_Q8_0 || p.fmt == GROUT_WFMT_Q4_K ||
+                 p.fmt == GROUT_WFMT_Q6_K,
+             GROUT_ENOTSUP, "%s%s%d: format %d is not f16, Q8_0, Q4_K or Q6_K", what, lname,
+             layer, p.fmt);
+  GROUT_NEED(p.rows >= 1, GROUT_EINVAL, "%s%s%d: rows=%d", what, lname, layer, p.rows);
+  GROUT_NEED(p.data != nullptr && aligned16(p.data), GROUT_EINVAL,
+             "%s%s%d: data is NULL or not 16-byte aligned", what, lname, layer);
+  if (p.fmt == GROUT_WFMT_F16)
+    GROUT_NEED(k % 8 == 0, GROUT_ENOTSUP, "%s%s%d: f16 needs k %% 8 == 0 (k=%d)", what, lname,
+               layer, k);
+  else
+    GROUT_NEED(grout::qweight_bytes(p.fmt, p.rows, k) != 0, GROUT_ENOTSUP,
+               "%s%s%d: format %d does not fit k=%d (a multiple of the block size, at most "
+               "16384)",
+               what, lname, layer, p.fmt, k);
+  return GROUT_OK;
+}
+
+Mat to_mat(const grout_wpart& p) { return Mat{p.fmt, p.rows, p.data}; }
+
+// The mixed-format API's weights, checked part by part.
+int convert_q(const grout_qwen3_config* c, const grout_qwen3_qweights* w, Mat& embed,
+              Mat& lm_head, std::vector<LayerW>& layers) {
+  GROUT_NEED(w != nullptr, GROUT_EINVAL, "weights is NULL");
+  const int H = c->hidden_size, I = c->intermediate_size, V = c->vocab_size;
+  const int qd = c->num_q_heads * 128, qkv = qd + 2 * c->num_kv_heads * 128;
+  GROUT_CHECK(check_part(w->embed_tokens, H, "embed_tokens", -1));
+  GROUT_CHECK(check_part(w->lm_head, H, "lm_head", -1));
+  GROUT_NEED(w->embed_tokens.rows == V && w->lm_head.rows == V, GROUT_EINVAL,
+             "embed_tokens / lm_head rows %d / %d != vocab_size=%d", w->embed_tokens.rows,
+             w->lm_head.rows, V);
+  GROUT_CHECK(check_ptrs16({{w->norm, "norm"}}));
+  GROUT_NEED(w->layers != nullptr, GROUT_EINVAL, "layers is NULL");
+  embed = to_mat(w->embed_tokens);
+  lm_head = to_mat(w->lm_head);
+  layers.assign(c->num_layers, LayerW{});
+  for (int l = 0; l < c->num_layers; ++l) {
+    const grout_qwen3_qlayer& L = w->layers[l];
+    const int rc = check_ptrs16({{L.input_layernorm, "input_layernorm"},
+                                 {L.q_norm, "q_norm"},
+                                 {L.k_norm, "k_norm"},
+                                 {L.post_attention_layernorm, "post_attention_layernorm"}});
+    if (rc != GROUT_OK) return fail(rc, "layer %d: %s", l, g_last_error.c_str());
+    GROUT_NEED(L.num_qkv_parts >= 1 && L.num_qkv_parts <= 3, GROUT_EINVAL,
+               "layer %d: num_qkv_parts=%d", l, L.num_qkv_parts);
+    GROUT_NEED(L.num_gate_up_parts >= 1 && L.num_gate_up_parts <= 2, GROUT_EINVAL,
+               "layer %d: num_gate_up_parts=%d", l, L.num_gate_up_parts);
+    LayerW& o = layers[l];
+    o.input_norm = L.input_layernorm;
+    o.q_norm = L.q_norm;
+    o.k_norm = L.k_norm;
+    o.post_norm = L.post_attention_layernorm;
+    long sum = 0;
+    o.nqkv = L.num_qkv_parts;
+    for (int i = 0; i < o.nqkv; ++i) {
+      GROUT_CHECK(check_part(L.qkv[i], H, "qkv part", l));
+      o.qkv[i] = to_mat(L.qkv[i]);
+      sum += L.qkv[i].rows;
+    }
+    GROUT_NEED(sum == qkv, GROUT_EINVAL, "layer %d: qkv parts cover %ld rows, expected %d", l,
+               sum, qkv);
+    sum = 0;
+    o.ngu = L.num_gate_up_parts;
+    for (int i = 0; i < o.ngu; ++i) {
+      GROUT_CHECK(check_part(L.gate_up[i], H, "gate_up part", l));
+      o.gu[i] = to_mat(L.gate_up[i]);
+      sum += L.gate_up[i].rows;
+    }
+    GROUT_NEED(sum == 2L * I, GROUT_EINVAL, "layer %d: gate_up parts cover %ld rows, expected %d",
+               l, sum, 2 * I);
+    // two parts must split at the gate | up boundary (silu pairs row i with i + I)
+    GROUT_NEED(o.ngu == 1 || o.gu[0].rows == I, GROUT_EINVAL,
+               "layer %d: the first gate_up part has %d rows, expected %d (gate)", l,
+               o.gu[0].rows, I);
+    GROUT_CHECK(check_part(L.o_proj, qd, "o_proj", l));
+    GROUT_CHECK(check_part(L.down_proj, I, "down_proj", l));
+    GROUT_NEED(L.o_proj.rows == H && L.down_proj.rows == H, GROUT_EINVAL,
+               "layer %d: o_proj / down_proj rows %d / %d != hidden_size=%d", l, L.o_proj.rows,
+               L.down_proj.rows, H);
+    o.o = to_mat(L.o_proj);
+    o.down = to_mat(L.down_proj);
+  }
+  return GROUT_OK;
+}
+
+// Largest low-bit matrix the prefill dequantizes (bytes of its f16 form).
+size_t dequant_scratch_bytes(const grout_engine* e) {
+  const auto& c = e->cfg;
+  size_t mx = 0;
+  auto see = [&](const Mat& m, int k) {
+    if (m.fmt != GROUT_WFMT_F16) mx = std::max(mx, (size_t)m.rows * k * sizeof(uint16_t));
+  };
+  for (const LayerW& w : e->layers) {
+    for (int i = 0; i < w.nqkv; ++i) see(w.qkv[i], c.hidden_size);
+    for (int i = 0; i < w.ngu; ++i) see(w.gu[i], c.hidden_size);
+    see(w.o, e->q_dim);
+    see(w.down, c.intermediate_size);
+  }
+  return mx;
+}
+
+// Takes the converted weights (embed, lm_head, layers moved in).
+int create_impl(grout_engine* e, const grout_qwen3_config* c, const void* final_norm, Mat embed,
+                Mat lm_head, std::vector<LayerW>&& layers, int device) {
   e->cfg = *c;
   e->device = device;
-  e->embed = w->embed_tokens;
-  e->final_norm = w->norm;
-  e->lm_head = w->lm_head;
-  e->layers.assign(w->layers, w->layers + c->num_layers);
+  e->embed = embed;
+  e->final_norm = final_norm;
+  e->lm_head = lm_head;
+  e->layers = std::move(layers);
   e->q_dim = c->num_q_heads * 128;
   e->kv_dim = c->num_kv_heads * 128;
   e->qkv_dim = e->q_dim + 2 * e->kv_dim;
@@ -404,6 +617,7 @@ int create_impl(grout_engine* e, const grout_qwen3_config* c, const grout_qwen3_
   b.qkv = a.take(e->qkv_dim * h2);
   b.attn_out = a.take(e->q_dim * h2);
   b.attn_proj = a.take(H * h2);
+  b.gate_up = a.take(2 * I * h2);
   b.ff = a.take(I * h2);
   b.ff_down = a.take(H * h2);
   b.logits = a.take((size_t)c->vocab_size * h2);
@@ -422,6 +636,9 @@ int create_impl(grout_engine* e, const grout_qwen3_config* c, const grout_qwen3_
   GROUT_CHECK(hip_status(hipHostMalloc(reinterpret_cast<void**>(&e->h_token), sizeof(uint32_t),
                                        hipHostMallocDefault),
                          "hipHostMalloc(token)"));
+  e->deq_bytes = dequant_scratch_bytes(e);
+  if (e->deq_bytes)
+    GROUT_CHECK(hip_status(hipMalloc(&e->deq, e->deq_bytes), "hipMalloc(dequant scratch)"));
   GROUT_CHECK(hip_status(hipStreamSynchronize(e->stream), "hipStreamSynchronize"));
   return capture_decode_graph(e);
 }
@@ -556,6 +773,16 @@ int grout_gemv_q_silu_mul(int fmt, const void* wq, const void* x, void* y, int i
                     "gemv_q_silu_mul launch");
 }
 
+int grout_qweight_gather(int fmt, const void* wq, int n, int k, const uint32_t* ids, int rows,
+                         void* out, void* stream) {
+  GROUT_CHECK(check_q(fmt, n, k));
+  GROUT_NEED(rows >= 1, GROUT_EINVAL, "rows=%d", rows);
+  GROUT_CHECK(check_ptrs16({{wq, "wq"}, {out, "out"}}));
+  GROUT_NEED(ids != nullptr, GROUT_EINVAL, "ids is NULL");
+  return hip_status(grout::launch_qgather(fmt, wq, n, k, ids, rows, out, as_stream(stream)),
+                    "qweight gather launch");
+}
+
 int grout_qweight_dequant(int fmt, const void* wq, int n, int k, void* out, void* stream) {
   GROUT_CHECK(check_q(fmt, n, k));
   GROUT_CHECK(check_ptrs16({{wq, "wq"}, {out, "out"}}));
@@ -583,17 +810,25 @@ int grout_argmax(const void* logits, int vocab_size, void* workspace, size_t wor
                     "argmax launch");
 }
 
-int grout_engine_create(const grout_qwen3_config* config, const grout_qwen3_weights* weights,
-                        int device, grout_engine** out) {
+}  // extern "C"
+
+namespace {
+
+template <class Convert>
+int create_common(const grout_qwen3_config* config, const void* norm, int device,
+                  grout_engine** out, Convert convert) {
   GROUT_NEED(out != nullptr, GROUT_EINVAL, "out is NULL");
   *out = nullptr;
-  GROUT_CHECK(validate(config, weights));
+  GROUT_CHECK(validate_config(config));
+  Mat embed, lm_head;
+  std::vector<LayerW> layers;
+  GROUT_CHECK(convert(embed, lm_head, layers));
   int ndev = 0;
   GROUT_CHECK(hip_status(hipGetDeviceCount(&ndev), "hipGetDeviceCount"));
   GROUT_NEED(device >= 0 && device < ndev, GROUT_EINVAL, "device %d of %d", device, ndev);
   grout_engine* e = new (std::nothrow) grout_engine();
   GROUT_NEED(e != nullptr, GROUT_EINVAL, "out of host memory");
-  const int rc = create_impl(e, config, weights, device);
+  const int rc = create_impl(e, config, norm, embed, lm_head, std::move(layers), device);
   if (rc != GROUT_OK) {
     const std::string msg = g_last_error;
     grout_engine_destroy(e);
@@ -602,6 +837,26 @@ int grout_engine_create(const grout_qwen3_config* config, const grout_qwen3_weig
   }
   *out = e;
   return GROUT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int grout_engine_create(const grout_qwen3_config* config, const grout_qwen3_weights* weights,
+                        int device, grout_engine** out) {
+  const void* norm = weights ? weights->norm : nullptr;
+  return create_common(config, norm, device, out, [&](Mat& em, Mat& lm, std::vector<LayerW>& ls) {
+    return convert_f16(config, weights, em, lm, ls);
+  });
+}
+
+int grout_engine_create_q(const grout_qwen3_config* config, const grout_qwen3_qweights* weights,
+                          int device, grout_engine** out) {
+  const void* norm = weights ? weights->norm : nullptr;
+  return create_common(config, norm, device, out, [&](Mat& em, Mat& lm, std::vector<LayerW>& ls) {
+    return convert_q(config, weights, em, lm, ls);
+  });
 }
 
 }  // extern "C"
@@ -628,23 +883,39 @@ int run_chunk(grout_engine* e, const uint32_t* tokens, int n, int pos0, float* l
   GROUT_CHECK(hip_status(hipMemcpyAsync(e->p(b.ids), tokens, (size_t)n * sizeof(uint32_t),
                                         hipMemcpyHostToDevice, s),
                          "tokens H2D"));
-  GROUT_CHECK(hip_status(grout::launch_embedding(e->p<uint32_t>(b.ids), e->embed, e->p(b.hidden),
-                                                 n, c.hidden_size, c.vocab_size, s),
-                         "embedding"));
+  GROUT_CHECK(embed_rows(e, e->p<uint32_t>(b.ids), e->p(b.hidden), n));
   const int H = c.hidden_size, I = c.intermediate_size;
-  const size_t kv_rows_off = (size_t)e->q_dim * H;  // element offset of K rows in qkv_proj
+  const int qd = e->q_dim, kd = e->kv_dim;
+  // the q, k and v buffers as row ranges of the QKV output
+  struct Range {
+    int lo, hi;
+    void* buf;
+  } const qkv_dst[3] = {{0, qd, e->p(b.q)}, {qd, qd + kd, e->p(b.k)}, {qd + kd, qd + 2 * kd, e->p(b.v)}};
   for (int l = 0; l < c.num_layers; ++l) {
-    const grout_qwen3_layer& w = e->layers[l];
+    const LayerW& w = e->layers[l];
     if (l == 0)
-      GROUT_CHECK(norm(e, nullptr, e->p(b.hidden), w.input_layernorm, e->p(b.normed), nullptr, n));
+      GROUT_CHECK(norm(e, nullptr, e->p(b.hidden), w.input_norm, e->p(b.normed), nullptr, n));
     else
-      GROUT_CHECK(norm(e, e->p(b.hidden_after_attn), e->p(b.ff_down), w.input_layernorm,
+      GROUT_CHECK(norm(e, e->p(b.hidden_after_attn), e->p(b.ff_down), w.input_norm,
                        e->p(b.normed), e->p(b.hidden), n));
-    const uint16_t* wqkv = static_cast<const uint16_t*>(w.qkv_proj);
-    GROUT_CHECK(project(e, wqkv, e->p(b.normed), e->p(b.q), n, e->q_dim, H));
-    GROUT_CHECK(project(e, wqkv + kv_rows_off, e->p(b.normed), e->p(b.k), n, e->kv_dim, H));
-    GROUT_CHECK(project(e, wqkv + kv_rows_off + (size_t)e->kv_dim * H, e->p(b.normed), e->p(b.v),
-                        n, e->kv_dim, H));
+    // each part's rows into the q, k, v ranges they cover
+    int row0 = 0;
+    for (int i = 0; i < w.nqkv; ++i) {
+      const Mat& m = w.qkv[i];
+      const void* wf = nullptr;
+      GROUT_CHECK(mat_f16(e, m, H, &wf));
+      for (const Range& r : qkv_dst) {
+        const int lo = std::max(row0, r.lo), hi = std::min(row0 + m.rows, r.hi);
+        if (lo >= hi) continue;
+        const uint16_t* wr = static_cast<const uint16_t*>(wf) + (size_t)(lo - row0) * H;
+        uint16_t* y = static_cast<uint16_t*>(r.buf) + (lo - r.lo);
+        if (n == 1 && m.fmt == GROUT_WFMT_F16)
+          GROUT_CHECK(hip_status(grout::launch_gemv(wr, e->p(b.normed), y, hi - lo, H, s), "gemv"));
+        else
+          GROUT_CHECK(gemm_rows(e, wr, e->p(b.normed), y, n, hi - lo, H, r.hi - r.lo));
+      }
+      row0 += m.rows;
+    }
     GROUT_CHECK(grout_qk_norm_rope_kv_prefill(
         e->p(b.q), e->p(b.k), e->p(b.v), w.q_norm, w.k_norm, e->rope_cos(), e->rope_sin(),
         e->p(b.q_rope), e->k_cache(l), e->v_cache(l), pos0, n, c.num_q_heads, c.num_kv_heads,
@@ -652,13 +923,18 @@ int run_chunk(grout_engine* e, const uint32_t* tokens, int n, int pos0, float* l
     GROUT_CHECK(grout_fmha_prefill(e->p(b.q_rope), e->k_cache(l), e->v_cache(l),
                                    e->p(b.attn_out), n, pos0, c.num_q_heads, c.num_kv_heads, 128,
                                    e->head_stride, e->qk_scale, s));
-    GROUT_CHECK(project(e, w.o_proj, e->p(b.attn_out), e->p(b.attn_proj), n, H, e->q_dim));
-    GROUT_CHECK(norm(e, e->p(b.hidden), e->p(b.attn_proj), w.post_attention_layernorm,
-                     e->p(b.ff_normed), e->p(b.hidden_after_attn), n));
-    GROUT_CHECK(project(e, w.gate_up_proj, e->p(b.ff_normed), e->p(b.gate_up), n, 2 * I, H));
+    GROUT_CHECK(mat_project(e, w.o, e->p(b.attn_out), e->p(b.attn_proj), n, qd, H));
+    GROUT_CHECK(norm(e, e->p(b.hidden), e->p(b.attn_proj), w.post_norm, e->p(b.ff_normed),
+                     e->p(b.hidden_after_attn), n));
+    row0 = 0;
+    for (int i = 0; i < w.ngu; ++i) {
+      GROUT_CHECK(mat_project(e, w.gu[i], e->p(b.ff_normed), e->p<uint16_t>(b.gate_up) + row0, n,
+                              H, 2 * I));
+      row0 += w.gu[i].rows;
+    }
     GROUT_CHECK(hip_status(grout::launch_silu_mul(e->p(b.gate_up), e->p(b.ff), n, I, s),
                            "silu_mul"));
-    GROUT_CHECK(project(e, w.down_proj, e->p(b.ff), e->p(b.ff_down), n, H, I));
+    GROUT_CHECK(mat_project(e, w.down, e->p(b.ff), e->p(b.ff_down), n, I, H));
   }
   // Only the last token's logits are needed (src/model.rs api_prefill_logits).
   const size_t last = (size_t)(n - 1) * H;
@@ -727,6 +1003,7 @@ int grout_engine_destroy(grout_engine* e) {
   if (e->graph) (void)hipGraphDestroy(e->graph);
   if (e->blas) (void)rocblas_destroy_handle(e->blas);
   if (e->pre.base) (void)hipFree(e->pre.base);
+  if (e->deq) (void)hipFree(e->deq);
   if (e->dec.base) (void)hipFree(e->dec.base);
   if (e->rope) (void)hipFree(e->rope);
   if (e->kv) (void)hipFree(e->kv);

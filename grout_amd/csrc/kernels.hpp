@@ -73,6 +73,9 @@ hipError_t launch_qweight_repack(int fmt, const void* ggml_blocks, int N, int K,
 // silu: W holds 2N rows [gate | up] and y[n] = silu(gate_n) * up_n.
 hipError_t launch_gemv_q(int fmt, const void* W, const void* x, void* y, int N, int K, bool silu,
                          hipStream_t stream);
+// out[t] = row ids[t] of the N x K matrix as f16 (CPU dequantization rule).
+hipError_t launch_qgather(int fmt, const void* W, int N, int K, const uint32_t* ids, int rows,
+                          void* out, hipStream_t stream);
 hipError_t launch_qweight_dequant(int fmt, const void* W, int N, int K, void* out,
                                   hipStream_t stream);
 

@@ -545,19 +545,16 @@ __device__ __forceinline__ QRaw qload(const uint8_t* __restrict__ W, const QLayo
 
 
 
-// w[row][k] as f16 (for the prefill GEMMs): one thread per 16-byte piece.
-template <int FMT>
-__global__ __launch_bounds__(256) void qdequant_kernel(const uint8_t* __restrict__ W, int N,
-                                                      int K, QLayout L, half_t* __restrict__ out) {
-  // Each weight is fp32 arithmetic in the reference's order (no fused
-  // multiply-add), rounded once to f16.
+// Piece j of weight row `row` as f16 into o (the row's output).  Each weight
+// is fp32 arithmetic in the reference's order (no fused multiply-add), rounded
+// once to f16.  DECODE: the decode layout's Q4_K scales, f16(d * sc) and
+// f16(dmin * m); otherwise the CPU rule, d * sc and dmin * m in fp32 (the
+// reference's native-layout embedding gather, src/kernels.rs:1963-2007).
+template <int FMT, bool DECODE>
+__device__ __forceinline__ void dequant_piece(const uint8_t* __restrict__ W, const QLayout& L,
+                                              int row, int j, int K, half_t* __restrict__ o) {
 #pragma clang fp contract(off)
-  const int P = K / (FMT == 8 ? 16 : 32);
-  const size_t p = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (p >= (size_t)N * P) return;
-  const int row = (int)(p / P), j = (int)(p % P);
   const QRaw r = qload<FMT>(W, L, row, j, K);
-  half_t* o = out + (size_t)row * K;
   if (FMT == 8) {
     const float d = h2f_bits(*reinterpret_cast<const uint16_t*>(W + L.off[1] +
                                                                  ((size_t)row * (K / 32) + (j >> 1)) * 2));
@@ -580,9 +577,14 @@ __global__ __launch_bounds__(256) void qdequant_kernel(const uint8_t* __restrict
         m[t] = (sc[jj + 4] >> 4) | ((sc[jj] >> 6) << 4);
       }
     }
-    // effective scales of the decode layout: f16(d * sc), f16(dmin * m)
-    const float d1 = (float)f2h_signed(d * (float)s[0]), m1 = (float)f2h_signed(dmin * (float)m[0]);
-    const float d2 = (float)f2h_signed(d * (float)s[1]), m2 = (float)f2h_signed(dmin * (float)m[1]);
+    float d1 = d * (float)s[0], m1 = dmin * (float)m[0];
+    float d2 = d * (float)s[1], m2 = dmin * (float)m[1];
+    if (DECODE) {  // effective scales of the decode layout
+      d1 = (float)f2h_signed(d1);
+      m1 = (float)f2h_signed(m1);
+      d2 = (float)f2h_signed(d2);
+      m2 = (float)f2h_signed(m2);
+    }
     const uint8_t* q = reinterpret_cast<const uint8_t*>(&r.a);
     const int e0 = sb * 256 + 64 * g + l0;
     for (int i = 0; i < 16; ++i) {
@@ -607,6 +609,32 @@ __global__ __launch_bounds__(256) void qdequant_kernel(const uint8_t* __restrict
       o[e_hi + i] = f2h_signed(shi * (float)qhi);
     }
   }
+}
+
+// w[row][k] as f16 with the decode layout's scales (for the prefill GEMMs):
+// one thread per piece of 16 (Q8_0) or 32 weights.
+template <int FMT>
+__global__ __launch_bounds__(256) void qdequant_kernel(const uint8_t* __restrict__ W, int N,
+                                                      int K, QLayout L, half_t* __restrict__ out) {
+  const int P = K / (FMT == 8 ? 16 : 32);
+  const size_t p = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= (size_t)N * P) return;
+  const int row = (int)(p / P), j = (int)(p % P);
+  dequant_piece<FMT, true>(W, L, row, j, K, out + (size_t)row * K);
+}
+
+// out[t][k] = f16 of row ids[t] of the N-row matrix by the CPU rule (token
+// embedding gather); ids at or past N read row N - 1.
+template <int FMT>
+__global__ __launch_bounds__(256) void qgather_kernel(const uint8_t* __restrict__ W, int N, int K,
+                                                     QLayout L, const uint32_t* __restrict__ ids,
+                                                     int rows, half_t* __restrict__ out) {
+  const int P = K / (FMT == 8 ? 16 : 32);
+  const size_t p = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= (size_t)rows * P) return;
+  const int t = (int)(p / P), j = (int)(p % P);
+  const int row = (int)min(ids[t], (uint32_t)(N - 1));
+  dequant_piece<FMT, false>(W, L, row, j, K, out + (size_t)t * K);
 }
 
 // ---------------------------------------------------------------- launchers
@@ -717,6 +745,21 @@ hipError_t launch_gemv_q(int fmt, const void* W, const void* x, void* y, int N, 
     case 8: gemv_q_launch<8>(W, x, y, N, K, silu, stream); break;
     case 12: gemv_q_launch<12>(W, x, y, N, K, silu, stream); break;
     default: gemv_q_launch<14>(W, x, y, N, K, silu, stream); break;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_qgather(int fmt, const void* W, int N, int K, const uint32_t* ids, int rows,
+                          void* out, hipStream_t stream) {
+  if (!qfmt_ok(fmt, N, K) || rows < 1) return hipErrorInvalidValue;
+  const QLayout L = qlayout(fmt, (size_t)N, (size_t)K);
+  const size_t pieces = (size_t)rows * (K / (fmt == 8 ? 16 : 32));
+  const unsigned blocks = (unsigned)((pieces + 255) / 256);
+  const uint8_t* w = (const uint8_t*)W;
+  switch (fmt) {
+    case 8: qgather_kernel<8><<<blocks, 256, 0, stream>>>(w, N, K, L, ids, rows, (half_t*)out); break;
+    case 12: qgather_kernel<12><<<blocks, 256, 0, stream>>>(w, N, K, L, ids, rows, (half_t*)out); break;
+    default: qgather_kernel<14><<<blocks, 256, 0, stream>>>(w, N, K, L, ids, rows, (half_t*)out); break;
   }
   return hipGetLastError();
 }

@@ -24,7 +24,10 @@ import torch
 from ._lib import ModelInfo as _CModelInfo
 from ._lib import Qwen3Config as _CConfig
 from ._lib import Qwen3Layer as _CLayer
+from ._lib import Qwen3QLayer as _CQLayer
+from ._lib import Qwen3QWeights as _CQWeights
 from ._lib import Qwen3Weights as _CWeights
+from ._lib import WPart as _CWPart
 from ._lib import call, lib
 
 HEAD_DIM = 128
@@ -145,6 +148,116 @@ class Qwen3Weights:
                 need(L[k], shp, f"layer {i} {k}")
 
 
+# Weight formats (ggml type ids for the low-bit ones; include/grout_engine.h).
+F16, Q8_0, Q4_K, Q6_K = 0, 8, 12, 14
+QBLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}  # (weights, bytes) per block
+QLAYER_VECS = ("input_layernorm", "q_norm", "k_norm", "post_attention_layernorm")
+QLAYER_MATS = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+
+
+class QuantWeights:
+    """Mixed-format weights on the device for grout_engine_create_q, as a
+    GGUF file holds them (the reference's Weight / MatrixWeight,
+    src/weights.rs:7-56).
+
+    Every matrix is (fmt, data): fmt F16 with data an fp16 [rows][k] array
+    (numpy fp16 or uint16 bit patterns), or Q8_0 / Q4_K / Q6_K with data the
+    tensor's ggml blocks (uint8, rows contiguous).  q|k|v and gate|up runs of
+    one low-bit format are concatenated and repacked as one part (one GEMV in
+    the decode step); a format change starts a new part.  The norm vectors
+    are fp16.  lm_head None ties the head to embed_tokens (one device copy)."""
+
+    def __init__(self, cfg: Qwen3Config, embed_tokens, norm, layers: List[Dict],
+                 lm_head=None, device="cuda"):
+        self.cfg = cfg
+        self._keep: List[torch.Tensor] = []
+        self._device = device
+        H, I, V = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
+        qd, kd = cfg.q_dim, cfg.kv_dim
+        if len(layers) != cfg.num_layers:
+            raise ValueError(f"{len(layers)} layers, config has {cfg.num_layers}")
+        self.embed = self._group([(embed_tokens, V)], H, "embed_tokens")[0]
+        self.lm_head = self.embed if lm_head is None else \
+            self._group([(lm_head, V)], H, "lm_head")[0]
+        self.norm = self._vec(norm, H, "norm")
+        self.layers = []
+        for i, L in enumerate(layers):
+            d = {k: self._vec(L[k], HEAD_DIM if k in ("q_norm", "k_norm") else H,
+                              f"layer {i} {k}") for k in QLAYER_VECS}
+            d["qkv"] = self._group([(L["q_proj"], qd), (L["k_proj"], kd), (L["v_proj"], kd)], H,
+                                   f"layer {i} qkv")
+            d["gate_up"] = self._group([(L["gate_proj"], I), (L["up_proj"], I)], H,
+                                       f"layer {i} gate_up")
+            d["o_proj"] = self._group([(L["o_proj"], H)], qd, f"layer {i} o_proj")[0]
+            d["down_proj"] = self._group([(L["down_proj"], H)], I, f"layer {i} down_proj")[0]
+            self.layers.append(d)
+
+    def _vec(self, a, n, what) -> int:
+        t = torch.from_numpy(np.ascontiguousarray(a).view(np.float16).reshape(-1)).to(self._device)
+        if t.numel() != n:
+            raise ValueError(f"{what}: {t.numel()} values, expected {n}")
+        self._keep.append(t)
+        return t.data_ptr()
+
+    def _group(self, mats, k: int, what: str):
+        """[(fmt, rows, device pointer)] for matrices [((fmt, data), rows)] in row order."""
+        parts, i = [], 0
+        while i < len(mats):
+            fmt = int(mats[i][0][0])
+            j = i
+            while j + 1 < len(mats) and int(mats[j + 1][0][0]) == fmt:
+                j += 1
+            rows = sum(r for _, r in mats[i:j + 1])
+            if fmt == F16:
+                a = np.concatenate([np.ascontiguousarray(m[1]).view(np.uint16).reshape(r, k)
+                                    for m, r in mats[i:j + 1]])
+                t = torch.from_numpy(a.view(np.float16)).to(self._device)
+            elif fmt in QBLOCK:
+                be, bb = QBLOCK[fmt]
+                if k % be:
+                    raise ValueError(f"{what}: k={k} is not a multiple of {be}")
+                a = np.concatenate([np.ascontiguousarray(m[1], np.uint8).reshape(r, k // be * bb)
+                                    for m, r in mats[i:j + 1]])
+                raw = torch.from_numpy(a.reshape(-1)).to(self._device)
+                nbytes = lib().grout_qweight_bytes(fmt, rows, k)
+                if nbytes == 0:
+                    raise ValueError(f"{what}: format {fmt} does not fit k={k}")
+                t = torch.empty(nbytes, dtype=torch.uint8, device=self._device)
+                call("grout_qweight_repack", fmt, C.c_void_p(raw.data_ptr()), rows, k,
+                     C.c_void_p(t.data_ptr()), None)
+                torch.cuda.synchronize()
+                del raw
+            else:
+                raise ValueError(f"{what}: unsupported format {fmt}")
+            self._keep.append(t)
+            parts.append((fmt, rows, t.data_ptr()))
+            i = j + 1
+        return parts
+
+    def device_bytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in self._keep)
+
+    def c_struct(self):
+        """(grout_qwen3_qweights, the layer array it points to)."""
+        def wp(p):
+            return _CWPart(p[0], p[1], p[2])
+
+        layers = (_CQLayer * len(self.layers))()
+        for i, d in enumerate(self.layers):
+            L = layers[i]
+            for k in QLAYER_VECS:
+                setattr(L, k, d[k])
+            L.num_qkv_parts = len(d["qkv"])
+            for j, p in enumerate(d["qkv"]):
+                L.qkv[j] = wp(p)
+            L.num_gate_up_parts = len(d["gate_up"])
+            for j, p in enumerate(d["gate_up"]):
+                L.gate_up[j] = wp(p)
+            L.o_proj = wp(d["o_proj"])
+            L.down_proj = wp(d["down_proj"])
+        return _CQWeights(wp(self.embed), self.norm, wp(self.lm_head), layers), layers
+
+
 def _config_from_info(info) -> "tuple[Qwen3Config, int]":
     c = info.config
     eos = tuple(int(info.eos_token_ids[i]) for i in range(info.num_eos))
@@ -202,6 +315,26 @@ class Engine:
         self._h = C.c_void_p()
         call("grout_engine_create", C.byref(c), C.byref(w), device_ord, C.byref(self._h))
         self._logits = np.empty(cfg.vocab_size, np.float32)
+
+    @classmethod
+    def from_quantized(cls, cfg: Qwen3Config, weights: QuantWeights, max_ctx: int = 4096,
+                       device_ord: int = 0) -> "Engine":
+        """Engine over mixed-format (GGUF block) weights (grout_engine_create_q);
+        the weights are borrowed: this object keeps them alive."""
+        if max_ctx <= 0:
+            raise ValueError("max_ctx must be positive")
+        self = cls.__new__(cls)
+        self._h = C.c_void_p()
+        self.cfg = cfg
+        self.weights = weights
+        self._meta = ModelMeta(cfg.vocab_size, tuple(cfg.eos_token_ids), "qwen3", max_ctx)
+        c = _CConfig(cfg.num_layers, cfg.hidden_size, cfg.intermediate_size,
+                     cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim,
+                     cfg.vocab_size, cfg.rms_norm_eps, cfg.rope_theta, max_ctx)
+        w, self._layers = weights.c_struct()
+        call("grout_engine_create_q", C.byref(c), C.byref(w), device_ord, C.byref(self._h))
+        self._logits = np.empty(cfg.vocab_size, np.float32)
+        return self
 
     # -- src/api.rs:60-90
     @classmethod

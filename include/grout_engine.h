@@ -147,9 +147,19 @@ int grout_gemv_q(int fmt, const void* wq, const void* x, void* y, int n, int k, 
 int grout_gemv_q_silu_mul(int fmt, const void* wq, const void* x, void* y, int inter, int k,
                           void* stream);
 
-/* The [n][k] matrix dequantized to f16 (out), e.g. for prefill GEMMs
- * (the reference's prefill dequant scratch, src/loader.rs:162). */
+/* The [n][k] matrix dequantized to f16 (out) with the decode layout's scales,
+ * e.g. for prefill GEMMs: the reference's prefill dequant into its pooled
+ * scratch (dequant_q4k_soa_to_f16 / dequant_q6k_soa_to_f16 /
+ * dequant_q8_0_to_f16, src/kernels.rs:1075-1160; src/quant_scratch.rs). */
 int grout_qweight_dequant(int fmt, const void* wq, int n, int k, void* out, void* stream);
+
+/* out[t][0..k) = row ids[t] of the [n][k] matrix as f16 for t < rows, by the
+ * CPU dequantization rule (Q4_K with fp32 d*sc and dmin*m); ids (device
+ * memory) at or past n read row n - 1.  The token-embedding gather from a
+ * quantized table: embed_gather_q8_0_f16 / embed_gather_q4k_f16 /
+ * embed_gather_q6k_f16 (src/kernels.rs:1940-2060). */
+int grout_qweight_gather(int fmt, const void* wq, int n, int k, const uint32_t* ids, int rows,
+                         void* out, void* stream);
 
 /* Scratch bytes grout_argmax needs for vocab_size logits. */
 size_t grout_argmax_workspace_bytes(int vocab_size);
@@ -211,6 +221,50 @@ int grout_model_free(grout_model* model);
  * 2631-4006). */
 int grout_engine_create(const grout_qwen3_config* config, const grout_qwen3_weights* weights,
                         int device, grout_engine** out);
+
+/* One weight matrix of a projection: `rows` output rows over the
+ * projection's input width k, as f16 [rows][k] (fmt GROUT_WFMT_F16) or in
+ * grout_qweight_repack's layout (GROUT_WFMT_Q8_0 / Q4_K / Q6_K).  Mirrors
+ * Weight / MatrixWeight (src/weights.rs:7-56), whose parts may differ in
+ * format (a Q4_K_M file stores some attn_v and ffn_down matrices as Q6_K). */
+typedef struct {
+  int fmt;
+  int rows;
+  const void* data;
+} grout_wpart;
+
+/* One decoder layer over mixed-format weights.  qkv parts cover the q | k | v
+ * output rows in order (one part when q, k and v share a format and were
+ * repacked together); gate_up parts cover gate | up rows in order. */
+typedef struct {
+  const void* input_layernorm;          /* f16 [hidden] */
+  int num_qkv_parts;                    /* 1..3 */
+  grout_wpart qkv[3];                   /* k = hidden */
+  const void* q_norm;                   /* f16 [128] */
+  const void* k_norm;                   /* f16 [128] */
+  grout_wpart o_proj;                   /* [hidden] rows, k = Hq * 128 */
+  const void* post_attention_layernorm; /* f16 [hidden] */
+  int num_gate_up_parts;                /* 1..2 */
+  grout_wpart gate_up[2];               /* k = hidden */
+  grout_wpart down_proj;                /* [hidden] rows, k = intermediate */
+} grout_qwen3_qlayer;
+
+typedef struct {
+  grout_wpart embed_tokens;             /* [vocab] rows, k = hidden; gathered */
+  const void* norm;                     /* f16 [hidden] */
+  grout_wpart lm_head;                  /* [vocab] rows; embed_tokens when tied */
+  const grout_qwen3_qlayer* layers;     /* num_layers entries */
+} grout_qwen3_qweights;
+
+/* grout_engine_create over mixed-format weights.  Decode: the norms as their
+ * own kernels, then the low-bit GEMV per part (gate_up as one part: SiLU in
+ * the GEMV epilogue), f16 parts as in grout_engine_create; the embedding row
+ * is gathered from the table.  Prefill and extend: each low-bit part is
+ * dequantized to f16 into an engine scratch buffer and multiplied with the
+ * GEMM (the reference's prefill dequant scratch, src/quant_scratch.rs:17-105).
+ * Every part's format must fit its k (grout_qweight_bytes != 0). */
+int grout_engine_create_q(const grout_qwen3_config* config, const grout_qwen3_qweights* weights,
+                          int device, grout_engine** out);
 
 /* Engine::load (src/api.rs:60-90): grout_model_load + grout_engine_create
  * with max_ctx (0 = max_position_embeddings); the engine owns the model and

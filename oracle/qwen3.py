@@ -96,12 +96,20 @@ def argmax(logits_bits: np.ndarray) -> int:
 
 
 class Qwen3Oracle:
-    """Host weights (fp16 bit patterns) + per-layer KV caches [Hkv][max_ctx][128]."""
+    """Host weights (fp16 bit patterns) + per-layer KV caches [Hkv][max_ctx][128].
 
-    def __init__(self, cfg, host: Dict, max_ctx: int):
+    decode_w64 (low-bit weights): {key: fp64 matrix} for keys (l, "qkv_proj"),
+    (l, "o_proj"), (l, "gate_up_proj"), (l, "down_proj") and "lm_head".  A
+    decode step multiplies by these (the decode GEMVs compute with the fp32
+    dequantized weights), and so does the head after a prefill (one row,
+    the GEMV); prefill and extend rows multiply by the fp16 matrices in
+    `host` (the dequantized weights rounded to f16 for the GEMM)."""
+
+    def __init__(self, cfg, host: Dict, max_ctx: int, decode_w64: Optional[Dict] = None):
         self.cfg = cfg
         self.w = host
         self.max_ctx = max_ctx
+        self.decode_w64 = decode_w64 or {}
         Hkv = cfg.num_key_value_heads
         self.k = [np.zeros((Hkv, max_ctx, D), np.uint16) for _ in range(cfg.num_layers)]
         self.v = [np.zeros((Hkv, max_ctx, D), np.uint16) for _ in range(cfg.num_layers)]
@@ -109,8 +117,10 @@ class Qwen3Oracle:
         self.next_pos = 0
         self._w64: Dict = {}
 
-    def _lin(self, x_bits, key, w_bits):
+    def _lin(self, x_bits, key, w_bits, decode: bool = False):
         """linear() with the fp64 copy of each weight made once."""
+        if decode and key in self.decode_w64:
+            return linear(x_bits, w_bits, self.decode_w64[key])
         if key not in self._w64:
             self._w64[key] = np.ascontiguousarray(w_bits, np.uint16).view(np.float16).astype(
                 np.float64)
@@ -124,9 +134,10 @@ class Qwen3Oracle:
     def head_weight(self) -> np.ndarray:
         return self.w["lm_head"] if self.w.get("lm_head") is not None else self.w["embed_tokens"]
 
-    def forward(self, tokens: Sequence[int], pos0: int, nthreads: int = 1):
+    def forward(self, tokens: Sequence[int], pos0: int, nthreads: int = 1, decode: bool = False):
         """Runs len(tokens) tokens at positions pos0.. and returns (f16 logits
-        of the last one as fp32, greedy token)."""
+        of the last one as fp32, greedy token); decode: the one-token decode
+        step (its projections use decode_w64)."""
         c = self.cfg
         ids = np.asarray(tokens, np.int64)
         S = ids.size
@@ -140,7 +151,7 @@ class Qwen3Oracle:
                 normed = rms_norm(hidden, L["input_layernorm"], eps)
             else:
                 normed, hidden = add_rms_norm(hidden_after_attn, ff_down, L["input_layernorm"], eps)
-            qkv = self._lin(normed, (l, "qkv_proj"), L["qkv_proj"])
+            qkv = self._lin(normed, (l, "qkv_proj"), L["qkv_proj"], decode)
             q = np.ascontiguousarray(qkv[:, :qd]).reshape(S, Hq, D)
             k = np.ascontiguousarray(qkv[:, qd:qd + kd]).reshape(S, Hkv, D)
             v = np.ascontiguousarray(qkv[:, qd + kd:]).reshape(S, Hkv, D)
@@ -148,13 +159,13 @@ class Qwen3Oracle:
                                                self.sin, self.k[l], self.v[l], pos0, eps)
             attn = O.attention_prefill_rows(q_rope, self.k[l], self.v[l], pos0, nthreads=nthreads)
             attn_bits = f16_bits(attn.reshape(S, qd))
-            attn_proj = self._lin(attn_bits, (l, "o_proj"), L["o_proj"])
+            attn_proj = self._lin(attn_bits, (l, "o_proj"), L["o_proj"], decode)
             ff_normed, hidden_after_attn = add_rms_norm(hidden, attn_proj,
                                                         L["post_attention_layernorm"], eps)
-            ff = silu_mul(self._lin(ff_normed, (l, "gate_up_proj"), L["gate_up_proj"]), I)
-            ff_down = self._lin(ff, (l, "down_proj"), L["down_proj"])
+            ff = silu_mul(self._lin(ff_normed, (l, "gate_up_proj"), L["gate_up_proj"], decode), I)
+            ff_down = self._lin(ff, (l, "down_proj"), L["down_proj"], decode)
         normed, _ = add_rms_norm(hidden_after_attn[-1:], ff_down[-1:], self.w["norm"], eps)
-        logits = self._lin(normed, "lm_head", self.head_weight())[0]
+        logits = self._lin(normed, "lm_head", self.head_weight(), True)[0]
         self.next_pos = pos0 + S
         return _f(logits).astype(np.float32), argmax(logits)
 
@@ -162,7 +173,7 @@ class Qwen3Oracle:
         return self.forward(tokens, 0, nthreads)
 
     def decode(self, token: int, nthreads: int = 1):
-        return self.forward([token], self.next_pos, nthreads)
+        return self.forward([token], self.next_pos, nthreads, decode=True)
 
 
 def random_host_weights(cfg, seed: int, std: float = 0.02, norm_lo: float = 0.8,

@@ -1,0 +1,147 @@
+"""GPU parity of the Qwen3 engine over mixed-format (GGUF block) weights
+(grout_engine_create_q) against the CPU oracle, through the C ABI.
+
+Weights: seeded N(0, std) matrices quantized by tests/qutil.py into the plan's
+formats, Q4_K_M-style mixes (q/k Q4_K with v Q6_K, gate/up in one format or
+two, f16 parts among low-bit ones, tied and untied heads).  The oracle
+multiplies decode steps (and the head) by the fp32 dequantized weights the
+GEMVs use, prefill and extend rows by those weights rounded to f16 (the
+dequant + GEMM path), and gathers embeddings by the CPU dequantization rule.
+Tolerances as the f16 engine's (tests/test_gpu_model.py)."""
+import numpy as np
+import pytest
+
+import oracle as O
+from oracle import qwen3 as Q
+import qutil
+from test_gpu_model import check_logits, check_token
+
+pytestmark = pytest.mark.gpu
+
+F16, Q8, Q4, Q6 = qutil.F16, O.Q8_0, O.Q4_K, O.Q6_K
+
+
+def configs():
+    from grout_amd.model import Qwen3Config
+
+    return {
+        "g2": Qwen3Config(num_layers=2, hidden_size=256, intermediate_size=512,
+                          num_attention_heads=4, num_key_value_heads=2, vocab_size=300),
+        "k1024": Qwen3Config(num_layers=2, hidden_size=1024, intermediate_size=2048,
+                             num_attention_heads=8, num_key_value_heads=2, vocab_size=16500),
+        "4b-dims-2l": Qwen3Config(num_layers=2, hidden_size=2560, intermediate_size=9728,
+                                  num_attention_heads=32, num_key_value_heads=8,
+                                  vocab_size=32000),
+    }
+
+
+Q4KM = {"q": Q4, "k": Q4, "v": Q6, "o": Q4, "gate": Q4, "up": Q4, "down": Q6}
+MIXED = {"q": Q8, "k": Q8, "v": Q8, "o": Q6, "gate": Q4, "up": Q8, "down": F16}
+SPLIT = {"q": Q6, "k": F16, "v": Q4, "o": F16, "gate": Q6, "up": Q6, "down": Q4}
+
+PLANS = {
+    "q4km-tied": {"embed": Q4, "lm_head": None, "layers": [Q4KM, MIXED]},
+    "mixed-untied": {"embed": Q8, "lm_head": Q6, "layers": [SPLIT, Q4KM]},
+    "f16-embed": {"embed": F16, "lm_head": Q8, "layers": [MIXED, SPLIT]},
+}
+
+
+def build(name, plan_name, seed, max_ctx):
+    from grout_amd.model import Engine, QuantWeights
+
+    cfg = configs()[name]
+    std = 0.05 if cfg.hidden_size < 2048 else 0.02
+    spec, host, w64 = qutil.mixed_weights(cfg, PLANS[plan_name], seed, std)
+    qw = QuantWeights(cfg, **spec)
+    eng = Engine.from_quantized(cfg, qw, max_ctx=max_ctx)
+    orc = Q.Qwen3Oracle(cfg, host, max_ctx, decode_w64=w64)
+    return cfg, eng, orc
+
+
+@pytest.mark.parametrize("name,plan,n_prompt,n_decode,max_ctx", [
+    ("g2", "q4km-tied", 37, 5, 64), ("g2", "mixed-untied", 1, 3, 16),
+    ("g2", "f16-embed", 20, 3, 64), ("k1024", "q4km-tied", 70, 4, 256),
+    ("k1024", "mixed-untied", 33, 3, 256), ("4b-dims-2l", "q4km-tied", 41, 3, 1024)])
+def test_qengine_prefill_and_decode_vs_oracle(gpu, name, plan, n_prompt, n_decode, max_ctx):
+    print(f"qengine {name} {plan} prompt={n_prompt} decode={n_decode}", flush=True)
+    cfg, eng, orc = build(name, plan, 5 + n_prompt, max_ctx)
+    prompt = np.random.default_rng(n_prompt).integers(0, cfg.vocab_size, n_prompt)
+    try:
+        got = eng.prefill(prompt).values
+        ref, _ = orc.prefill(prompt, nthreads=8)
+        tol = check_logits(got, ref, f"q {name} {plan} prefill")
+        tok = int(np.argmax(got))
+        check_token(tok, ref, tol, "prefill token")
+        for i in range(n_decode):
+            got = eng.decode(tok).values
+            ref, _ = orc.decode(tok, nthreads=8)
+            tol = check_logits(got, ref, f"q {name} {plan} decode {i}")
+            tok = int(np.argmax(got))
+            check_token(tok, ref, tol, f"decode token {i}")
+        assert eng.position == n_prompt + n_decode
+    finally:
+        eng.close()
+
+
+def test_qengine_extend_and_greedy_vs_oracle(gpu):
+    """Extend chunks (dequant + GEMM rows at pos0 > 0, one of them a single
+    token) between decode steps; decode_greedy agrees with the oracle."""
+    cfg, eng, orc = build("k1024", "mixed-untied", 9, 256)
+    rng = np.random.default_rng(4)
+    try:
+        prompt = rng.integers(0, cfg.vocab_size, 25)
+        got = eng.prefill(prompt).values
+        ref, _ = orc.prefill(prompt, nthreads=8)
+        check_logits(got, ref, "q prefill")
+        tok = int(np.argmax(got))
+        got = eng.decode(tok).values
+        ref, _ = orc.decode(tok, nthreads=8)
+        check_logits(got, ref, "q decode")
+        for chunk in (rng.integers(0, cfg.vocab_size, 17), [int(np.argmax(got))]):
+            got = eng.extend(chunk).values
+            ref, _ = orc.forward(chunk, orc.next_pos, nthreads=8)
+            tol = check_logits(got, ref, f"q extend {len(chunk)}")
+        tok = int(np.argmax(got))
+        nxt = eng.decode_greedy(tok)
+        ref, _ = orc.decode(tok, nthreads=8)
+        check_token(nxt, ref, tol, "decode_greedy token")
+        assert eng.position == 25 + 1 + 17 + 1 + 1
+    finally:
+        eng.close()
+
+
+def test_qengine_argument_errors(gpu):
+    """Shape, format and part-layout errors are reported by name."""
+    import ctypes as C
+
+    from grout_amd._lib import GroutError, Qwen3Config as CConfig, call
+    from grout_amd.model import Qwen3Config, QuantWeights
+
+    cfg = configs()["g2"]
+    spec, _, _ = qutil.mixed_weights(cfg, PLANS["q4km-tied"], 1, 0.05)
+    qw = QuantWeights(cfg, **spec)
+    c = CConfig(cfg.num_layers, cfg.hidden_size, cfg.intermediate_size, cfg.num_attention_heads,
+                cfg.num_key_value_heads, cfg.head_dim, cfg.vocab_size, cfg.rms_norm_eps,
+                cfg.rope_theta, 16)
+
+    def create(mutate, match):
+        w, layers = qw.c_struct()
+        mutate(w, layers)
+        h = C.c_void_p()
+        with pytest.raises(GroutError, match=match):
+            call("grout_engine_create_q", C.byref(c), C.byref(w), 0, C.byref(h))
+
+    create(lambda w, L: setattr(L[0], "num_qkv_parts", 0), "num_qkv_parts")
+    create(lambda w, L: setattr(L[1].down_proj, "fmt", 13), "format 13")
+    create(lambda w, L: setattr(L[0].o_proj, "rows", 128), "o_proj")
+    create(lambda w, L: setattr(L[0].qkv[0], "rows", L[0].qkv[0].rows - 1), "qkv parts cover")
+    create(lambda w, L: setattr(w.lm_head, "rows", 299), "vocab_size")
+    create(lambda w, L: setattr(L[1].gate_up[0], "data", None), "gate_up part")
+    # a low-bit matrix whose k is not a multiple of its block size is refused
+    odd = Qwen3Config(num_layers=1, hidden_size=384, intermediate_size=512, num_attention_heads=4,
+                      num_key_value_heads=2, vocab_size=64)
+    plan = {"embed": F16, "lm_head": None, "layers": [{k: F16 for k in Q4KM}]}
+    spec2, _, _ = qutil.mixed_weights(odd, plan, 1, 0.05)
+    spec2["layers"][0]["q_proj"] = (Q4, np.zeros((odd.q_dim, 384 // 256 * 144), np.uint8))
+    with pytest.raises(ValueError, match="not a multiple of 256"):
+        QuantWeights(odd, **spec2)

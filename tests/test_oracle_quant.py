@@ -152,3 +152,17 @@ def test_bad_sizes_are_rejected():
         O.dequant(O.Q4_K, np.zeros(144, np.uint8), 100)
     with pytest.raises(ValueError):
         O.dequant(3, np.zeros(144, np.uint8), 256)
+
+
+@pytest.mark.parametrize("fmt,bound", [(O.Q8_0, 0.01), (O.Q4_K, 0.1), (O.Q6_K, 0.03)])
+def test_test_quantizer_round_trip(fmt, bound):
+    """tests/qutil.py's quantizer (used to build engine test weights) decodes,
+    through the oracle, to within its quantization noise of the input."""
+    import qutil
+
+    w = (np.random.default_rng(fmt).standard_normal((6, 1024)) * 0.05).astype(np.float32)
+    b = qutil.quantize(fmt, w)
+    be, bb = O.qblock(fmt)
+    assert b.shape == (6, 1024 // be * bb)
+    d = O.dequant(fmt, b, w.size).reshape(w.shape)
+    assert np.sqrt(((d - w) ** 2).mean() / (w ** 2).mean()) < bound
