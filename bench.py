@@ -36,7 +36,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--only", default="",
-                    help="comma list: decode32b,prefill,decode4b,norm,engine4b (gemv, qgemv: only "
+                    help="comma list: decode32b,prefill,decode4b,norm,engine4b,engine4b_q4km (gemv, qgemv: only "
                          "when named)")
     ap.add_argument("--eager", action="store_true",
                     help="launch the timed calls from the host instead of replaying a captured "
@@ -257,6 +257,59 @@ def bench_engine(prompt_len=512, decode_steps=256, max_ctx=1024):
                 distinct_tokens=len(set(toks)), mean_ctx=mean_ctx)
 
 
+def q4km_formats(n_layers):
+    """Q4_K_M-style mix: attn_v and ffn_down in Q6_K for the first and last
+    eighth of the layers and every third layer between, Q4_K elsewhere."""
+    Q4, Q6 = 12, 14
+
+    def more_bits(l):
+        return l < n_layers // 8 or l >= 7 * n_layers // 8 or (l - n_layers // 8) % 3 == 2
+
+    def fmts(l):
+        hi = Q6 if more_bits(l) else Q4
+        return {"q": Q4, "k": Q4, "v": hi, "o": Q4, "gate": Q4, "up": Q4, "down": hi}
+    return fmts
+
+
+def bench_engine_q(prompt_len=512, decode_steps=256, max_ctx=1024):
+    """Config 5 over low-bit weights: the Qwen3-4B engine with random
+    GGUF-block weights in a Q4_K_M-style mix (q4km_formats; Q6_K tied
+    embedding / lm_head), prompt and timing as bench_engine."""
+    import numpy as np
+    import torch
+    from grout_amd.model import Engine, QuantWeights, Qwen3Config
+
+    cfg = Qwen3Config.qwen3_4b()
+    qw = QuantWeights.random(cfg, q4km_formats(cfg.num_layers), embed_fmt=14, seed=0)
+    torch.cuda.synchronize()
+    eng = Engine.from_quantized(cfg, qw, max_ctx=max_ctx)
+    prompt = np.random.default_rng(512).integers(0, cfg.vocab_size, prompt_len)
+    eng.warmup()
+    tok = eng.prefill_greedy(prompt)
+    for _ in range(8):
+        tok = eng.decode_greedy(tok)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    tok = eng.prefill_greedy(prompt)
+    prefill_s = time.perf_counter() - t0
+    toks = [tok]
+    t0 = time.perf_counter()
+    for _ in range(decode_steps):
+        toks.append(eng.decode_greedy(toks[-1]))
+    decode_s = time.perf_counter() - t0
+    eng.close()
+    # per decode token: every repacked weight byte once (the tied table is
+    # read whole by the lm_head GEMV) + K and V of the live context
+    weight_bytes = qw.device_bytes()
+    mean_ctx = prompt_len + decode_steps / 2
+    kv_bytes = cfg.num_layers * 2 * cfg.num_key_value_heads * mean_ctx * D * 2
+    del qw, eng
+    torch.cuda.empty_cache()
+    return dict(prefill_ms=prefill_s * 1e3, decode_ms=decode_s * 1e3 / decode_steps,
+                tok_s=decode_steps / decode_s, bytes_per_token=weight_bytes + kv_bytes,
+                weight_bytes=weight_bytes, distinct_tokens=len(set(toks)), mean_ctx=mean_ctx)
+
+
 def bench_gemv(steps, warmup):
     """The decode step's projections on Qwen3-4B shapes, each over 8 rotating
     weight copies (> the 256 MB Infinity Cache for all but the smallest), as
@@ -439,6 +492,9 @@ def main():
         res["engine4b"]["attn_graph_ms"] = 36 * bench_fused_attention(
             32, 8, int(res["engine4b"]["mean_ctx"]), 1024, 36, a.steps, a.warmup)
         print(f"# engine4b {res['engine4b']}", file=sys.stderr, flush=True)
+    if want("engine4b_q4km"):
+        res["engine4b_q4km"] = bench_engine_q()
+        print(f"# engine4b_q4km {res['engine4b_q4km']}", file=sys.stderr, flush=True)
 
     line = {"metric": "decode-attn HBM GB/s (% of peak) + prefill FMHA TFLOP/s (% MFMA peak)",
             "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "higher_is_better": True,
@@ -493,6 +549,17 @@ def main():
             "weight_stream_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
             "attention_share": round(r["attn_graph_ms"] / r["decode_ms"], 4),
             "attention_us_per_token": round(r["attn_graph_ms"] * 1e3, 1)}
+    if "engine4b_q4km" in res:
+        r = res["engine4b_q4km"]
+        gbs = r["bytes_per_token"] * r["tok_s"] / 1e9
+        line["engine4b_q4km"] = {
+            "workload": "qwen3-4b engine, random GGUF-block weights in a Q4_K_M-style mix "
+                        "(Q4_K; attn_v / ffn_down Q6_K in 18 of 36 layers; Q6_K tied embedding), "
+                        "512-token prompt, 256 greedy decode steps (decode-step hipGraph)",
+            "decode_tok_s": round(r["tok_s"], 1), "decode_ms_per_token": round(r["decode_ms"], 4),
+            "prefill_512_ms": round(r["prefill_ms"], 2),
+            "weight_bytes": r["weight_bytes"],
+            "weight_stream_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
     if not a.no_cpu and "decode32b" in res:
         cb = cpu_baseline_decode(64, 8, 32768)
         line["cpu_baseline"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in cb.items()}

@@ -107,6 +107,8 @@ SIGNATURES = {
     "grout_gemv_q_silu_mul": (_i, [_i, _p, _p, _p, _i, _i, _p]),
     "grout_qweight_dequant": (_i, [_i, _p, _i, _i, _p, _p]),
     "grout_qweight_gather": (_i, [_i, _p, _i, _i, _p, _i, _p, _p]),
+    "grout_gemv_q_rms_norm": (_i, [_i, _p, _p, _p, _p, _p, _p, _i, _i, _f, _p]),
+    "grout_gemv_q_rms_norm_silu_mul": (_i, [_i, _p, _p, _p, _p, _p, _p, _i, _i, _f, _p]),
     "grout_argmax_workspace_bytes": (_sz, [_i]),
     "grout_argmax": (_i, [_p, _i, _p, _sz, _p, _p]),
     "grout_engine_create": (_i, [C.POINTER(Qwen3Config), C.POINTER(Qwen3Weights), _i,

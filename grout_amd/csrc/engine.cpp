@@ -252,9 +252,27 @@ int head(grout_engine* e, const void* hidden_after_attn, const void* ff_down) {
                     "argmax");
 }
 
-// The decode step, as recorded into the graph.  A projection held as one f16
-// matrix takes the fused norm + GEMV kernels; otherwise the norm runs on its
-// own and each part takes the GEMV of its format.
+// One token through one weight part with the input RMSNorm folded into the
+// GEMV (x' = norm(residual + x) * gamma, or norm(x) * gamma without a
+// residual); f16(residual + x) goes to residual_out.  Every part of a
+// projection recomputes x' and writes the same residual_out bits.
+int mat_gemv_norm(grout_engine* e, const Mat& m, const void* residual, const void* x,
+                  const void* gamma, void* residual_out, void* y, int k, bool silu_rows) {
+  const float eps = e->cfg.rms_norm_eps;
+  if (m.fmt == GROUT_WFMT_F16)
+    return hip_status(grout::launch_gemv_norm(m.data, residual, x, gamma, residual_out, eps, y,
+                                              silu_rows ? m.rows / 2 : m.rows, k, silu_rows,
+                                              e->stream),
+                      "gemv_norm");
+  return hip_status(grout::launch_gemv_q_norm(m.fmt, m.data, residual, x, gamma, residual_out, eps,
+                                              y, silu_rows ? m.rows / 2 : m.rows, k, silu_rows,
+                                              e->stream),
+                    "gemv_q_norm");
+}
+
+// The decode step, as recorded into the graph.  The input and
+// post-attention norms fold into the first GEMV of their projection (every
+// part of a multi-part projection recomputes them).
 int record_decode_step(grout_engine* e) {
   const auto& c = e->cfg;
   const DecodeBufs& b = e->db;
@@ -268,18 +286,11 @@ int record_decode_step(grout_engine* e) {
     const void* res = l == 0 ? nullptr : e->d(b.hidden_after_attn);
     const void* xin = l == 0 ? e->d(b.hidden) : e->d(b.ff_down);
     void* res_out = l == 0 ? nullptr : e->d(b.hidden);
-    if (single_f16(w.qkv, w.nqkv)) {
-      GROUT_CHECK(hip_status(grout::launch_gemv_norm(w.qkv[0].data, res, xin, w.input_norm,
-                                                     res_out, c.rms_norm_eps, e->d(b.qkv),
-                                                     e->qkv_dim, H, false, s),
-                             "qkv gemv"));
-    } else {
-      GROUT_CHECK(norm(e, res, xin, w.input_norm, e->d(b.normed), res_out, 1));
-      size_t row = 0;
-      for (int i = 0; i < w.nqkv; ++i) {
-        GROUT_CHECK(mat_gemv(e, w.qkv[i], e->d(b.normed), e->d<uint16_t>(b.qkv) + row, H));
-        row += (size_t)w.qkv[i].rows;
-      }
+    size_t row = 0;
+    for (int i = 0; i < w.nqkv; ++i) {
+      GROUT_CHECK(mat_gemv_norm(e, w.qkv[i], res, xin, w.input_norm, res_out,
+                                e->d<uint16_t>(b.qkv) + row, H, false));
+      row += (size_t)w.qkv[i].rows;
     }
     // QK-norm/RoPE + K/V cache write inside the split-K attention, then the merge
     GROUT_CHECK(grout_attn_decode_fused(
@@ -289,26 +300,17 @@ int record_decode_step(grout_engine* e) {
         e->num_splits, c.rms_norm_eps, e->qk_scale, s));
     GROUT_CHECK(mat_gemv(e, w.o, e->d(b.attn_out), e->d(b.attn_proj), e->q_dim));
     // post-attention add + RMSNorm, gate_up and SiLU(gate) * up into ff
-    if (single_f16(w.gu, w.ngu)) {
-      GROUT_CHECK(hip_status(grout::launch_gemv_norm(w.gu[0].data, e->d(b.hidden),
-                                                     e->d(b.attn_proj), w.post_norm,
-                                                     e->d(b.hidden_after_attn), c.rms_norm_eps,
-                                                     e->d(b.ff), I, H, true, s),
-                             "gate_up gemv"));
+    if (w.ngu == 1) {  // SiLU(gate) * up in the GEMV epilogue
+      GROUT_CHECK(mat_gemv_norm(e, w.gu[0], e->d(b.hidden), e->d(b.attn_proj), w.post_norm,
+                                e->d(b.hidden_after_attn), e->d(b.ff), H, true));
     } else {
-      GROUT_CHECK(norm(e, e->d(b.hidden), e->d(b.attn_proj), w.post_norm, e->d(b.normed),
-                       e->d(b.hidden_after_attn), 1));
-      if (w.ngu == 1) {
-        GROUT_CHECK(hip_status(grout::launch_gemv_q(w.gu[0].fmt, w.gu[0].data, e->d(b.normed),
-                                                    e->d(b.ff), I, H, true, s),
-                               "gate_up gemv_q"));
-      } else {
-        GROUT_CHECK(mat_gemv(e, w.gu[0], e->d(b.normed), e->d(b.gate_up), H));
-        GROUT_CHECK(mat_gemv(e, w.gu[1], e->d(b.normed), e->d<uint16_t>(b.gate_up) + w.gu[0].rows,
-                             H));
-        GROUT_CHECK(hip_status(grout::launch_silu_mul(e->d(b.gate_up), e->d(b.ff), 1, I, s),
-                               "silu_mul"));
-      }
+      GROUT_CHECK(mat_gemv_norm(e, w.gu[0], e->d(b.hidden), e->d(b.attn_proj), w.post_norm,
+                                e->d(b.hidden_after_attn), e->d(b.gate_up), H, false));
+      GROUT_CHECK(mat_gemv_norm(e, w.gu[1], e->d(b.hidden), e->d(b.attn_proj), w.post_norm,
+                                e->d(b.hidden_after_attn), e->d<uint16_t>(b.gate_up) + w.gu[0].rows,
+                                H, false));
+      GROUT_CHECK(hip_status(grout::launch_silu_mul(e->d(b.gate_up), e->d(b.ff), 1, I, s),
+                             "silu_mul"));
     }
     GROUT_CHECK(mat_gemv(e, w.down, e->d(b.ff), e->d(b.ff_down), I));
   }
@@ -771,6 +773,41 @@ int grout_gemv_q_silu_mul(int fmt, const void* wq, const void* x, void* y, int i
              "y is NULL or not 2-byte aligned");
   return hip_status(grout::launch_gemv_q(fmt, wq, x, y, inter, k, true, as_stream(stream)),
                     "gemv_q_silu_mul launch");
+}
+
+static int check_q_norm(const void* wq, const void* residual, const void* x, const void* gamma,
+                        const void* residual_out, const void* y, float eps) {
+  GROUT_CHECK(check_ptrs16({{wq, "wq"}, {x, "x"}, {gamma, "gamma"}}));
+  if (residual) GROUT_CHECK(check_ptrs16({{residual, "residual"}}));
+  if (residual_out) {
+    GROUT_CHECK(check_ptrs16({{residual_out, "residual_out"}}));
+    GROUT_NEED(residual_out != residual && residual_out != x, GROUT_EINVAL,
+               "residual_out must not alias residual or x");
+  }
+  GROUT_NEED(y != nullptr && (reinterpret_cast<uintptr_t>(y) & 1u) == 0, GROUT_EALIGN,
+             "y is NULL or not 2-byte aligned");
+  GROUT_NEED(std::isfinite(eps) && eps > 0.f, GROUT_EINVAL, "eps=%g", (double)eps);
+  return GROUT_OK;
+}
+
+int grout_gemv_q_rms_norm(int fmt, const void* wq, const void* residual, const void* x,
+                          const void* gamma, void* residual_out, void* y, int n, int k, float eps,
+                          void* stream) {
+  GROUT_CHECK(check_q(fmt, n, k));
+  GROUT_CHECK(check_q_norm(wq, residual, x, gamma, residual_out, y, eps));
+  return hip_status(grout::launch_gemv_q_norm(fmt, wq, residual, x, gamma, residual_out, eps, y, n,
+                                              k, false, as_stream(stream)),
+                    "gemv_q_rms_norm launch");
+}
+
+int grout_gemv_q_rms_norm_silu_mul(int fmt, const void* wq, const void* residual, const void* x,
+                                   const void* gamma, void* residual_out, void* y, int inter,
+                                   int k, float eps, void* stream) {
+  GROUT_CHECK(check_q(fmt, 2 * inter, k));
+  GROUT_CHECK(check_q_norm(wq, residual, x, gamma, residual_out, y, eps));
+  return hip_status(grout::launch_gemv_q_norm(fmt, wq, residual, x, gamma, residual_out, eps, y,
+                                              inter, k, true, as_stream(stream)),
+                    "gemv_q_rms_norm_silu_mul launch");
 }
 
 int grout_qweight_gather(int fmt, const void* wq, int n, int k, const uint32_t* ids, int rows,

@@ -73,6 +73,12 @@ hipError_t launch_qweight_repack(int fmt, const void* ggml_blocks, int N, int K,
 // silu: W holds 2N rows [gate | up] and y[n] = silu(gate_n) * up_n.
 hipError_t launch_gemv_q(int fmt, const void* W, const void* x, void* y, int N, int K, bool silu,
                          hipStream_t stream);
+// As launch_gemv_q with the input RMSNorm folded in: x' = f16(x * inv *
+// gamma) (residual NULL) or, for c = residual + x, x' = f16(c * inv * gamma)
+// with f16(c) written to residual_out when it is not NULL.
+hipError_t launch_gemv_q_norm(int fmt, const void* W, const void* residual, const void* x,
+                              const void* gamma, void* residual_out, float eps, void* y, int N,
+                              int K, bool silu, hipStream_t stream);
 // out[t] = row ids[t] of the N x K matrix as f16 (CPU dequantization rule).
 hipError_t launch_qgather(int fmt, const void* W, int N, int K, const uint32_t* ids, int rows,
                           void* out, hipStream_t stream);

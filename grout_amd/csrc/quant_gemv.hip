@@ -395,7 +395,7 @@ __device__ __forceinline__ void stage_store(const SRaw& s, int u, int U, int UPR
 // Weight loads in flight per lane (NPW: pieces per lane and slice, 0 = any K).
 template <int FMT, int R, int NPW>
 constexpr int qbatch() {
-  constexpr int cap = R == 4 ? (FMT == 12 ? 20 : 10) : (FMT == 12 ? 8 : 4);
+  constexpr int cap = R == 4 ? (FMT == 12 ? 20 : 8) : (FMT == 12 ? 8 : 4);
   return NPW > 0 && NPW < cap ? NPW : cap;
 }
 
@@ -417,18 +417,84 @@ __device__ __forceinline__ void qconsume(QPc (&raw)[B], float& acc, int st, int 
   }
 }
 
+// Input RMSNorm folded into the staging of x (the NORM kernels): c =
+// residual + x in fp32 (residual NULL reads zeros: c = x exactly),
+// x' = f16(c * inv * gamma), inv = 1 / rms(c), and f16(c) to residual_out
+// when it is not NULL.  Every workgroup computes inv itself (in a fixed
+// order: lane sums, wave butterflies, waves in order); the first writes
+// residual_out.
+struct QNorm {
+  const half_t* res;
+  const half_t* gamma;
+  half_t* res_out;
+  float eps;
+};
+
+// The residual of a norm without one (read-only zeros, never written).
+__device__ half_t kQZero[kQMaxK];
+
+__device__ __forceinline__ float qwave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// c of chunk (8 values) and its contribution to sum(c^2).
+__device__ __forceinline__ float qnorm_c(u32x4 xv, u32x4 rv, float (&c)[8]) {
+  const half8 xh = as_half8(xv), rh = as_half8(rv);
+  float part = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    c[e] = (float)rh[e] + (float)xh[e];
+    part += c[e] * c[e];
+  }
+  return part;
+}
+
+// 1 / rms over the workgroup from each thread's partial sum (s_nrm: one float
+// per wave); every thread of the workgroup calls it.
+template <int T>
+__device__ __forceinline__ float qnorm_inv(float ss, int K, float eps, float* s_nrm) {
+  ss = qwave_sum(ss);
+  if ((threadIdx.x & 63) == 0) s_nrm[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  ss = s_nrm[0];
+#pragma unroll
+  for (int w = 1; w < T / 64; ++w) ss += s_nrm[w];
+  return 1.0f / sqrtf(ss / (float)K + eps);
+}
+
+// x' of one chunk; the first workgroup also writes f16(c) to residual_out.
+__device__ __forceinline__ u32x4 qnorm_apply(u32x4 xv, u32x4 rv, u32x4 gv, float inv, int c, int NG,
+                                             const QNorm& nz) {
+  float cv[8];
+  (void)qnorm_c(xv, rv, cv);
+  const half8 gh = as_half8(gv);
+  half8 o, co;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    o[e] = (half_t)(cv[e] * inv * (float)gh[e]);
+    co[e] = (half_t)cv[e];
+  }
+  if (nz.res_out != nullptr && blockIdx.x == 0 && c < NG)
+    *reinterpret_cast<u32x4*>(nz.res_out + 8 * c) = as_u32x4(co);
+  return as_u32x4(o);
+}
+
 // R weight rows per workgroup, each split into S slices of NPW pieces per
 // lane (one slice per group of R teams; K a multiple of 512 with
-// NPW * S >= K / 512 >= NPW), or NPW = 0: any K, S = 1.
-template <int FMT, bool SILU, int R, int S, int NPW>
+// NPW * S >= K / 512 >= NPW), or NPW = 0: any K, S = 1.  NORM: x is the
+// RMSNorm of residual + x (QNorm).
+template <int FMT, bool SILU, int R, int S, int NPW, bool NORM>
 __global__ __launch_bounds__(R * S * kQTeam) void gemv_q_kernel(const uint8_t* __restrict__ W,
                                                                const half_t* __restrict__ x,
                                                                half_t* __restrict__ y, int N,
-                                                               int K, QLayout L) {
+                                                               int K, QLayout L, QNorm nz) {
   constexpr int T = R * S * kQTeam;
   constexpr int B = qbatch<FMT, R, NPW>();
   // LDS: x (K halves, padded to whole swizzle runs), x sums, each local row's
-  // scales (SCW floats), then S x R slice partials.
+  // scales (SCW floats), then S x R slice partials and one float per wave
+  // for the norm.
   extern __shared__ __attribute__((aligned(16))) unsigned char s_dyn[];
   const int KX = (K + 127) & ~127;
   half_t* const s_x = reinterpret_cast<half_t*>(s_dyn);
@@ -453,9 +519,16 @@ __global__ __launch_bounds__(R * S * kQTeam) void gemv_q_kernel(const uint8_t* _
     // slice pieces i0 .. i0 + NPW - 1 clipped to NP: a slice that would run
     // past the end starts at NP - NPW and counts only pieces >= i0
     const int i0 = slice * NPW, st = min(i0, NP - NPW);
-    u32x4 xr[NXJ];
+    u32x4 xr[NXJ], rr[NORM ? NXJ : 1], gr[NORM ? NXJ : 1];
 #pragma unroll
     for (int j = 0; j < NXJ; ++j) xr[j] = load16(x + 8 * min(tid + T * j, NG - 1));
+    if constexpr (NORM) {
+      const half_t* res = nz.res != nullptr ? nz.res : kQZero;
+#pragma unroll
+      for (int j = 0; j < NXJ; ++j) rr[j] = load16(res + 8 * min(tid + T * j, NG - 1));
+#pragma unroll
+      for (int j = 0; j < NXJ; ++j) gr[j] = load16(nz.gamma + 8 * min(tid + T * j, NG - 1));
+    }
     SRaw ur[NUJ];
 #pragma unroll
     for (int j = 0; j < NUJ; ++j)
@@ -464,6 +537,18 @@ __global__ __launch_bounds__(R * S * kQTeam) void gemv_q_kernel(const uint8_t* _
 #pragma unroll
     for (int b = 0; b < B; ++b) raw[b] = qpc_load<FMT>(W, L, row, m + 16 * (st + b), K);
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (NORM) {
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < NXJ; ++j) {
+        float cv[8];
+        const float part = qnorm_c(xr[j], rr[j], cv);
+        ss += tid + T * j < NG ? part : 0.f;
+      }
+      const float inv = qnorm_inv<T>(ss, K, nz.eps, s_sc + R * SCW + S * R);
+#pragma unroll
+      for (int j = 0; j < NXJ; ++j) xr[j] = qnorm_apply(xr[j], rr[j], gr[j], inv, tid + T * j, NG, nz);
+    }
 #pragma unroll
     for (int j = 0; j < NXJ; ++j) stage_x<FMT>(xr[j], tid + T * j, NG, s_x, s_xsum);
 #pragma unroll
@@ -475,9 +560,24 @@ __global__ __launch_bounds__(R * S * kQTeam) void gemv_q_kernel(const uint8_t* _
                              s_xsum + fs * st, s_row + fs * st, W, L, row, K);
   } else {
     const int nxj = (NG + T - 1) / T;
+    float inv = 0.f;
+    const half_t* res = nz.res != nullptr ? nz.res : kQZero;
+    if constexpr (NORM) {  // a first pass for 1 / rms
+      float ss = 0.f;
+      for (int j = 0; j < nxj; ++j) {
+        const int c = tid + T * j, cc = min(c, NG - 1);
+        float cv[8];
+        const float part = qnorm_c(load16(x + 8 * cc), load16(res + 8 * cc), cv);
+        ss += c < NG ? part : 0.f;
+      }
+      inv = qnorm_inv<T>(ss, K, nz.eps, s_sc + R * SCW + S * R);
+    }
     for (int j = 0; j < nxj; ++j) {
-      const int c = tid + T * j;
-      stage_x<FMT>(load16(x + 8 * min(c, NG - 1)), c, NG, s_x, s_xsum);
+      const int c = tid + T * j, cc = min(c, NG - 1);
+      u32x4 xv = load16(x + 8 * cc);
+      if constexpr (NORM)
+        xv = qnorm_apply(xv, load16(res + 8 * cc), load16(nz.gamma + 8 * cc), inv, c, NG, nz);
+      stage_x<FMT>(xv, c, NG, s_x, s_xsum);
     }
     for (int u = tid; u < U; u += T)
       stage_store<FMT>(stage_load<FMT, SILU, R>(W, L, u, UPR, N, K), u, U, UPR, SCW, s_sc);
@@ -669,22 +769,26 @@ static bool npw_short(int v) {
   return v == 2 || v == 3 || v == 4 || v == 5 || v == 8 || v == 10 || v == 13;
 }
 
-template <int FMT, bool SILU, int R, int S>
+template <int FMT, bool SILU, int R, int S, bool NORM>
 static void gemv_q_go(int npw, unsigned grid, size_t lds, const void* W, const void* x, void* y,
-                      int N, int K, const QLayout& L, hipStream_t stream) {
+                      int N, int K, const QLayout& L, const QNorm& nz, hipStream_t stream) {
   const uint8_t* w = (const uint8_t*)W;
   const half_t* xi = (const half_t*)x;
   half_t* yo = (half_t*)y;
   constexpr int T = R * S * kQTeam;
 #define GROUT_QGO(V) \
-  case V: gemv_q_kernel<FMT, SILU, R, S, V><<<grid, T, lds, stream>>>(w, xi, yo, N, K, L); break;
+  case V:                                                                                     \
+    gemv_q_kernel<FMT, SILU, R, S, V, NORM><<<grid, T, lds, stream>>>(w, xi, yo, N, K, L, nz); \
+    break;
   if constexpr (R == 16) {
     switch (npw) {
       GROUT_QGO(5) GROUT_QGO(8) GROUT_QGO(10) GROUT_QGO(16) GROUT_QGO(19)
-      default: gemv_q_kernel<FMT, SILU, R, 1, 0><<<grid, T, lds, stream>>>(w, xi, yo, N, K, L);
+      default:
+        gemv_q_kernel<FMT, SILU, R, 1, 0, NORM><<<grid, T, lds, stream>>>(w, xi, yo, N, K, L, nz);
     }
   } else if constexpr (SILU || S == 0) {
-    gemv_q_kernel<FMT, SILU, R, 1, 0><<<grid, R * kQTeam, lds, stream>>>(w, xi, yo, N, K, L);
+    gemv_q_kernel<FMT, SILU, R, 1, 0, NORM><<<grid, R * kQTeam, lds, stream>>>(w, xi, yo, N, K, L,
+                                                                             nz);
   } else {
     switch (npw) {
       GROUT_QGO(2) GROUT_QGO(3) GROUT_QGO(4) GROUT_QGO(5) GROUT_QGO(8) GROUT_QGO(10)
@@ -699,12 +803,12 @@ static void gemv_q_go(int npw, unsigned grid, size_t lds, const void* W, const v
 template <int FMT>
 static size_t gemv_q_lds(int R, int S, int K) {
   return (size_t)((K + 127) & ~127) * 2 + (size_t)(FMT == 8 ? K / 32 : K / 16) * 4 +
-         (size_t)R * (FMT == 8 ? K / 32 : K / 16) * 4 + (size_t)R * S * 4;
+         (size_t)R * (FMT == 8 ? K / 32 : K / 16) * 4 + (size_t)R * S * 4 + 4 * 4;
 }
 
-template <int FMT>
+template <int FMT, bool NORM>
 static void gemv_q_launch(const void* W, const void* x, void* y, int N, int K, bool silu,
-                          hipStream_t stream) {
+                          const QNorm& nz, hipStream_t stream) {
   const int rows = silu ? 2 * N : N;
   const QLayout L = qlayout(FMT, (size_t)rows, (size_t)K);
   const int np = K % 512 == 0 ? K / 512 : 0;  // pieces per lane of a whole row
@@ -713,8 +817,8 @@ static void gemv_q_launch(const void* W, const void* x, void* y, int N, int K, b
     const int per = silu ? 8 : 16;
     const unsigned grid = (unsigned)((N + per - 1) / per);
     const int npw = npw_tall(np) ? np : 0;
-    if (silu) gemv_q_go<FMT, true, 16, 1>(npw, grid, gemv_q_lds<FMT>(16, 1, K), W, x, y, N, K, L, stream);
-    else gemv_q_go<FMT, false, 16, 1>(npw, grid, gemv_q_lds<FMT>(16, 1, K), W, x, y, N, K, L, stream);
+    if (silu) gemv_q_go<FMT, true, 16, 1, NORM>(npw, grid, gemv_q_lds<FMT>(16, 1, K), W, x, y, N, K, L, nz, stream);
+    else gemv_q_go<FMT, false, 16, 1, NORM>(npw, grid, gemv_q_lds<FMT>(16, 1, K), W, x, y, N, K, L, nz, stream);
     return;
   }
   // short: 4 rows per workgroup, each row split over S waves so that the grid
@@ -722,7 +826,7 @@ static void gemv_q_launch(const void* W, const void* x, void* y, int N, int K, b
   const int per = silu ? 2 : 4;
   const unsigned grid = (unsigned)((N + per - 1) / per);
   if (silu) {
-    gemv_q_go<FMT, true, 4, 0>(0, grid, gemv_q_lds<FMT>(4, 1, K), W, x, y, N, K, L, stream);
+    gemv_q_go<FMT, true, 4, 0, NORM>(0, grid, gemv_q_lds<FMT>(4, 1, K), W, x, y, N, K, L, nz, stream);
     return;
   }
   int S = 0, npw = 0;
@@ -732,19 +836,36 @@ static void gemv_q_launch(const void* W, const void* x, void* y, int N, int K, b
       if (v <= np && npw_short(v)) S = s, npw = v;
     }
   }
-  if (S == 0) gemv_q_go<FMT, false, 4, 0>(0, grid, gemv_q_lds<FMT>(4, 1, K), W, x, y, N, K, L, stream);
-  else if (S == 1) gemv_q_go<FMT, false, 4, 1>(npw, grid, gemv_q_lds<FMT>(4, 1, K), W, x, y, N, K, L, stream);
-  else if (S == 2) gemv_q_go<FMT, false, 4, 2>(npw, grid, gemv_q_lds<FMT>(4, 2, K), W, x, y, N, K, L, stream);
-  else gemv_q_go<FMT, false, 4, 4>(npw, grid, gemv_q_lds<FMT>(4, 4, K), W, x, y, N, K, L, stream);
+  if (S == 0) gemv_q_go<FMT, false, 4, 0, NORM>(0, grid, gemv_q_lds<FMT>(4, 1, K), W, x, y, N, K, L, nz, stream);
+  else if (S == 1) gemv_q_go<FMT, false, 4, 1, NORM>(npw, grid, gemv_q_lds<FMT>(4, 1, K), W, x, y, N, K, L, nz, stream);
+  else if (S == 2) gemv_q_go<FMT, false, 4, 2, NORM>(npw, grid, gemv_q_lds<FMT>(4, 2, K), W, x, y, N, K, L, nz, stream);
+  else gemv_q_go<FMT, false, 4, 4, NORM>(npw, grid, gemv_q_lds<FMT>(4, 4, K), W, x, y, N, K, L, nz, stream);
 }
 
 hipError_t launch_gemv_q(int fmt, const void* W, const void* x, void* y, int N, int K, bool silu,
                          hipStream_t stream) {
+  return launch_gemv_q_norm(fmt, W, nullptr, x, nullptr, nullptr, 0.f, y, N, K, silu, stream);
+}
+
+hipError_t launch_gemv_q_norm(int fmt, const void* W, const void* residual, const void* x,
+                              const void* gamma, void* residual_out, float eps, void* y, int N,
+                              int K, bool silu, hipStream_t stream) {
+  const QNorm nz{(const half_t*)residual, (const half_t*)gamma, (half_t*)residual_out, eps};
   if (!qfmt_ok(fmt, silu ? 2 * N : N, K)) return hipErrorInvalidValue;
+  const bool norm = gamma != nullptr;
   switch (fmt) {
-    case 8: gemv_q_launch<8>(W, x, y, N, K, silu, stream); break;
-    case 12: gemv_q_launch<12>(W, x, y, N, K, silu, stream); break;
-    default: gemv_q_launch<14>(W, x, y, N, K, silu, stream); break;
+    case 8:
+      if (norm) gemv_q_launch<8, true>(W, x, y, N, K, silu, nz, stream);
+      else gemv_q_launch<8, false>(W, x, y, N, K, silu, nz, stream);
+      break;
+    case 12:
+      if (norm) gemv_q_launch<12, true>(W, x, y, N, K, silu, nz, stream);
+      else gemv_q_launch<12, false>(W, x, y, N, K, silu, nz, stream);
+      break;
+    default:
+      if (norm) gemv_q_launch<14, true>(W, x, y, N, K, silu, nz, stream);
+      else gemv_q_launch<14, false>(W, x, y, N, K, silu, nz, stream);
+      break;
   }
   return hipGetLastError();
 }

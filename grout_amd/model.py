@@ -193,7 +193,11 @@ class QuantWeights:
             self.layers.append(d)
 
     def _vec(self, a, n, what) -> int:
-        t = torch.from_numpy(np.ascontiguousarray(a).view(np.float16).reshape(-1)).to(self._device)
+        if isinstance(a, torch.Tensor):
+            t = a.to(device=self._device, dtype=torch.float16).reshape(-1).contiguous()
+        else:
+            t = torch.from_numpy(np.ascontiguousarray(a).view(np.float16).reshape(-1)).to(
+                self._device)
         if t.numel() != n:
             raise ValueError(f"{what}: {t.numel()} values, expected {n}")
         self._keep.append(t)
@@ -208,17 +212,26 @@ class QuantWeights:
             while j + 1 < len(mats) and int(mats[j + 1][0][0]) == fmt:
                 j += 1
             rows = sum(r for _, r in mats[i:j + 1])
+            dev = isinstance(mats[i][0][1], torch.Tensor)  # blocks already on the device
             if fmt == F16:
-                a = np.concatenate([np.ascontiguousarray(m[1]).view(np.uint16).reshape(r, k)
-                                    for m, r in mats[i:j + 1]])
-                t = torch.from_numpy(a.view(np.float16)).to(self._device)
+                if dev:
+                    t = torch.cat([m[1].to(self._device, torch.float16).reshape(r, k)
+                                   for m, r in mats[i:j + 1]]).contiguous()
+                else:
+                    a = np.concatenate([np.ascontiguousarray(m[1]).view(np.uint16).reshape(r, k)
+                                        for m, r in mats[i:j + 1]])
+                    t = torch.from_numpy(a.view(np.float16)).to(self._device)
             elif fmt in QBLOCK:
                 be, bb = QBLOCK[fmt]
                 if k % be:
                     raise ValueError(f"{what}: k={k} is not a multiple of {be}")
-                a = np.concatenate([np.ascontiguousarray(m[1], np.uint8).reshape(r, k // be * bb)
-                                    for m, r in mats[i:j + 1]])
-                raw = torch.from_numpy(a.reshape(-1)).to(self._device)
+                if dev:
+                    raw = torch.cat([m[1].to(self._device).reshape(r, k // be * bb)
+                                     for m, r in mats[i:j + 1]]).reshape(-1)
+                else:
+                    a = np.concatenate([np.ascontiguousarray(m[1], np.uint8).reshape(
+                        r, k // be * bb) for m, r in mats[i:j + 1]])
+                    raw = torch.from_numpy(a.reshape(-1)).to(self._device)
                 nbytes = lib().grout_qweight_bytes(fmt, rows, k)
                 if nbytes == 0:
                     raise ValueError(f"{what}: format {fmt} does not fit k={k}")
@@ -236,6 +249,60 @@ class QuantWeights:
 
     def device_bytes(self) -> int:
         return sum(t.numel() * t.element_size() for t in self._keep)
+
+    @staticmethod
+    def random_blocks(fmt: int, rows: int, k: int, std: float, gen: torch.Generator,
+                      device="cuda") -> torch.Tensor:
+        """Seeded random ggml blocks on the device: random payload and 6-bit
+        scale bytes, block scales d (and dmin) set so the weights spread about
+        std (Q4_K: centred by dmin = 7.5 d).  For timing and smoke runs."""
+        if fmt == F16:
+            return torch.empty((rows, k), dtype=torch.float16, device=device).normal_(
+                0.0, std, generator=gen)
+        be, bb = QBLOCK[fmt]
+        b = torch.randint(0, 256, (rows * (k // be), bb), dtype=torch.uint8, device=device,
+                          generator=gen)
+
+        def f16(v):
+            return torch.tensor([v], dtype=torch.float16).view(torch.uint8).to(device)
+
+        if fmt == Q8_0:      # int8 uniform: std ~74 units
+            b[:, 0:2] = f16(std / 74.0)
+        elif fmt == Q4_K:    # q uniform 0..15, 6-bit scales uniform 0..63
+            d = std / (32.0 * 4.6)
+            b[:, 0:2] = f16(d)
+            b[:, 2:4] = f16(7.5 * d)
+        else:                # Q6_K: (q - 32) std ~18.5, int8 scales |sc| ~64
+            b[:, 208:210] = f16(std / (74.0 * 18.5))
+        return b.reshape(rows, -1)
+
+    @classmethod
+    def random(cls, cfg: Qwen3Config, layer_formats, embed_fmt: int, head_fmt=None,
+               seed: int = 0, std: float = 0.02, device="cuda") -> "QuantWeights":
+        """Random weights in the given formats: layer_formats(l) -> {"q", "k",
+        "v", "o", "gate", "up", "down": fmt}; head_fmt None = tied head."""
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+        H, I, V, qd, kd = (cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.q_dim,
+                           cfg.kv_dim)
+
+        def vec(n):
+            return torch.ones(n, dtype=torch.float16, device=device)
+
+        def mat(fmt, rows, k):
+            return (fmt, cls.random_blocks(fmt, rows, k, std, g, device))
+
+        layers = []
+        for l in range(cfg.num_layers):
+            f = layer_formats(l)
+            layers.append({"input_layernorm": vec(H), "q_norm": vec(HEAD_DIM),
+                           "k_norm": vec(HEAD_DIM), "post_attention_layernorm": vec(H),
+                           "q_proj": mat(f["q"], qd, H), "k_proj": mat(f["k"], kd, H),
+                           "v_proj": mat(f["v"], kd, H), "o_proj": mat(f["o"], H, qd),
+                           "gate_proj": mat(f["gate"], I, H), "up_proj": mat(f["up"], I, H),
+                           "down_proj": mat(f["down"], H, I)})
+        head = None if head_fmt is None else mat(head_fmt, V, H)
+        return cls(cfg, mat(embed_fmt, V, H), vec(H), layers, head, device)
 
     def c_struct(self):
         """(grout_qwen3_qweights, the layer array it points to)."""

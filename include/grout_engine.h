@@ -147,6 +147,21 @@ int grout_gemv_q(int fmt, const void* wq, const void* x, void* y, int n, int k, 
 int grout_gemv_q_silu_mul(int fmt, const void* wq, const void* x, void* y, int inter, int k,
                           void* stream);
 
+/* grout_gemv_q with the input RMSNorm folded in, as grout_gemv_rms_norm:
+ * x' = f16(norm(x) * gamma) (residual NULL) or, for c = residual + x (fp32),
+ * x' = f16(norm(c) * gamma) with f16(c) written to residual_out unless it is
+ * NULL (it must not alias residual or x).  The decode step's
+ * add_rms_norm_decode_raw_f16 (src/kernels.rs:4518-4657) and the low-bit
+ * projection GEMV in one launch. */
+int grout_gemv_q_rms_norm(int fmt, const void* wq, const void* residual, const void* x,
+                          const void* gamma, void* residual_out, void* y, int n, int k, float eps,
+                          void* stream);
+
+/* grout_gemv_q_silu_mul with the input RMSNorm folded in (as above). */
+int grout_gemv_q_rms_norm_silu_mul(int fmt, const void* wq, const void* residual, const void* x,
+                                   const void* gamma, void* residual_out, void* y, int inter,
+                                   int k, float eps, void* stream);
+
 /* The [n][k] matrix dequantized to f16 (out) with the decode layout's scales,
  * e.g. for prefill GEMMs: the reference's prefill dequant into its pooled
  * scratch (dequant_q4k_soa_to_f16 / dequant_q6k_soa_to_f16 /

@@ -159,3 +159,54 @@ def test_quant_argument_errors(gpu):
         lcall("grout_gemv_q", O.Q6_K, ptr(buf), ptr(buf), ptr(buf), 4, 100, None)
     with pytest.raises(GroutError, match="Q8_0"):
         lcall("grout_gemv_q", 2, ptr(buf), ptr(buf), ptr(buf), 4, 256, None)
+
+
+@pytest.mark.parametrize("fmt,name", FMTS)
+@pytest.mark.parametrize("n,k,silu,add", [(6144, 2560, False, True), (2560, 2560, False, False),
+                                          (9728, 2560, True, True), (16400, 2560, False, True),
+                                          (37, 256, False, True), (40, 256, True, False)])
+def test_gemv_q_rms_norm_vs_oracle(gpu, fmt, name, n, k, silu, add):
+    """Norm folded into the low-bit GEMV: x' as the oracle's (add_)rms_norm
+    within one f16 ulp per element (another fp32 summation order), so the
+    bound adds 2^-10 * sum |w x'|; residual_out bit-exact."""
+    from oracle import qwen3 as Q
+
+    L = gpu.lib()
+    rows = 2 * n if silu else n
+    print(f"gemv_q_rms_norm {name} n={n} k={k} silu={silu} add={add}", flush=True)
+    blocks = random_blocks(fmt, rows, k, seed=rows + k + fmt, dmax=4e-4 if silu else 2e-2)
+    rng = np.random.default_rng(k + n)
+    x = rng.standard_normal(k).astype(np.float16).view(np.uint16)
+    r = rng.standard_normal(k).astype(np.float16).view(np.uint16)
+    g = rng.uniform(0.5, 1.5, k).astype(np.float16).view(np.uint16)
+    wq = upload(fmt, blocks, rows, k, L)
+    xd, rd, gd = (torch.from_numpy(a.view(np.float16)).cuda() for a in (x, r, g))
+    ro = torch.zeros(k, dtype=torch.float16, device="cuda")
+    y = torch.empty(n, dtype=torch.float16, device="cuda")
+    fn = "grout_gemv_q_rms_norm_silu_mul" if silu else "grout_gemv_q_rms_norm"
+    call(L, fn, fmt, ptr(wq), ptr(rd) if add else None, ptr(xd), ptr(gd), ptr(ro) if add else None,
+         ptr(y), n, k, C.c_float(1e-6), None)
+    torch.cuda.synchronize()
+    if add:
+        xn, c = Q.add_rms_norm(r[None], x[None], g, 1e-6)
+        assert np.array_equal(ro.cpu().numpy().view(np.uint16), c[0])
+    else:
+        xn = Q.rms_norm(x[None], g, 1e-6)
+    xn = xn[0]
+    gu = O.gemv_q(fmt, blocks, rows, k, xn)
+    w = O.dequant(fmt, blocks, rows * k, decode=True).reshape(rows, k).astype(np.float64)
+    mag = (np.abs(w) + min_term(fmt, blocks, rows, k)) @ np.abs(O.h2f(xn).astype(np.float64))
+    tol_p = ulp(gu) + 1e-5 * mag + 2.0 ** -10 * mag
+    got = y.cpu().numpy().astype(np.float64)
+    if silu:
+        g16 = gu[:n].astype(np.float16).astype(np.float64)
+        u16 = gu[n:].astype(np.float16).astype(np.float64)
+        ref = (g16 / (1 + np.exp(-g16)) * u16).astype(np.float16).astype(np.float64)
+        sig = 1 / (1 + np.exp(-g16))
+        tol = np.abs(u16 * sig * (1 + g16 * (1 - sig))) * tol_p[:n] + np.abs(g16 * sig) * tol_p[n:] \
+            + 1.5 * ulp(ref) + 1e-7
+    else:
+        ref, tol = gu, tol_p
+    err = np.abs(got - ref)
+    print(f"[gemv_q_rms_norm {name}] max_err={err.max():.3e}", flush=True)
+    assert np.all(err <= tol)
