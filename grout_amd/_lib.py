@@ -119,6 +119,7 @@ SIGNATURES = {
     "grout_model_load": (_i, [C.c_char_p, _i, C.POINTER(_p)]),
     "grout_model_get_info": (_i, [_p, C.POINTER(ModelInfo)]),
     "grout_model_weights": (_i, [_p, C.POINTER(Qwen3Weights)]),
+    "grout_model_qweights": (_i, [_p, C.POINTER(Qwen3QWeights)]),
     "grout_model_free": (_i, [_p]),
     "grout_engine_load": (_i, [C.c_char_p, _i, _i, C.POINTER(_p)]),
     "grout_engine_model_info": (_i, [_p, C.POINTER(ModelInfo)]),

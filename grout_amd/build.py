@@ -34,6 +34,7 @@ SOURCES = [
     ("api.cpp", ["-x", "hip"]),
     ("engine.cpp", ["-x", "hip"]),
     ("loader.cpp", ["-x", "hip"]),
+    ("gguf.cpp", ["-x", "hip"]),
 ]
 # Prefill projections are plain GEMMs: rocBLAS.
 LIBS = ["-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"]

@@ -1059,13 +1059,19 @@ int grout_engine_load(const char* model_dir, int max_ctx, int device, grout_engi
   grout_model* m = nullptr;
   GROUT_CHECK(grout_model_load(model_dir, device, &m));
   grout_model_info info;
-  grout_qwen3_weights w;
   (void)grout_model_get_info(m, &info);
-  (void)grout_model_weights(m, &w);
   grout_qwen3_config cfg = info.config;
   if (max_ctx > 0) cfg.max_ctx = max_ctx;
   grout_engine* e = nullptr;
-  const int rc = grout_engine_create(&cfg, &w, device, &e);
+  grout_qwen3_weights w;
+  grout_qwen3_qweights qw;
+  int rc;
+  if (grout_model_weights(m, &w) == GROUT_OK) {
+    rc = grout_engine_create(&cfg, &w, device, &e);
+  } else {
+    (void)grout_model_qweights(m, &qw);
+    rc = grout_engine_create_q(&cfg, &qw, device, &e);
+  }
   if (rc != GROUT_OK) {
     const std::string msg = g_last_error;
     grout_model_free(m);

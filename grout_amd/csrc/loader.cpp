@@ -30,6 +30,7 @@
 #include "abi_util.hpp"
 #include "json.hpp"
 #include "kernels.hpp"
+#include "model_internal.hpp"
 
 using namespace grout_abi;
 
@@ -401,20 +402,12 @@ int plan_weights(Checkpoint& ck, Plan& pl) {
 
 }  // namespace
 
-struct grout_model {
-  grout_model_info info{};
-  int device = 0;
-  void* arena = nullptr;
-  std::vector<grout_qwen3_layer> layers;
-  const void* embed = nullptr;
-  const void* norm = nullptr;
-  const void* lm_head = nullptr;
-};
 
 extern "C" {
 
 int grout_model_inspect(const char* model_dir, grout_model_info* info) {
   GROUT_NEED(info != nullptr, GROUT_EINVAL, "info is NULL");
+  if (grout_gguf::is_gguf_path(model_dir)) return grout_gguf::inspect(model_dir, info);
   Checkpoint ck;
   GROUT_CHECK(ck.open(model_dir));
   Plan pl;
@@ -427,6 +420,7 @@ int grout_model_inspect(const char* model_dir, grout_model_info* info) {
 int grout_model_load(const char* model_dir, int device, grout_model** out) {
   GROUT_NEED(out != nullptr, GROUT_EINVAL, "out is NULL");
   *out = nullptr;
+  if (grout_gguf::is_gguf_path(model_dir)) return grout_gguf::load(model_dir, device, out);
   Checkpoint ck;
   GROUT_CHECK(ck.open(model_dir));
   Plan pl;
@@ -501,10 +495,21 @@ int grout_model_get_info(const grout_model* m, grout_model_info* info) {
 
 int grout_model_weights(const grout_model* m, grout_qwen3_weights* w) {
   GROUT_NEED(m != nullptr && w != nullptr, GROUT_EINVAL, "model or weights is NULL");
+  GROUT_NEED(!m->low_bit, GROUT_EINVAL, "the model holds GGUF weights: use grout_model_qweights");
   w->embed_tokens = m->embed;
   w->norm = m->norm;
   w->lm_head = m->lm_head;
   w->layers = m->layers.data();
+  return GROUT_OK;
+}
+
+int grout_model_qweights(const grout_model* m, grout_qwen3_qweights* w) {
+  GROUT_NEED(m != nullptr && w != nullptr, GROUT_EINVAL, "model or weights is NULL");
+  GROUT_NEED(m->low_bit, GROUT_EINVAL, "the model holds fp16 weights: use grout_model_weights");
+  w->embed_tokens = m->qembed;
+  w->norm = m->norm;
+  w->lm_head = m->qlm_head;
+  w->layers = m->qlayers.data();
   return GROUT_OK;
 }
 

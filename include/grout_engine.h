@@ -213,11 +213,19 @@ typedef struct grout_model grout_model;
  * model.safetensors) and checks that every tensor the engine needs is present
  * with the expected shape and a castable dtype (F16/BF16/F32/F64).  Mirrors
  * Loader::new + Qwen3Config::from_model_dir/validate (src/loader.rs:33-88,
- * src/config.rs:24-95). */
+ * src/config.rs:24-95).  A path ending in ".gguf" names a GGUF file (v2/v3)
+ * instead: the qwen3.* metadata becomes the config (config_from_gguf,
+ * src/loader.rs:276-330), eos = tokenizer.ggml.eos_token_id, the head is tied
+ * when output.weight is absent, and every tensor must be F32/F16/BF16 (norms)
+ * or F32/F16/BF16/Q8_0/Q4_K/Q6_K (matrices) with the config's shape; the
+ * reader's bounds are the reference's (src/gguf.rs:212-445).  weight_bytes is
+ * then the device bytes in the low-bit layouts. */
 int grout_model_inspect(const char* model_dir, grout_model_info* info);
 
 /* grout_model_inspect, then the weights into one device allocation on
- * `device` in the fused layouts (qkv_proj = q|k|v rows, gate_up_proj =
+ * `device` (GGUF: low-bit matrices in grout_qweight_repack's layout, one part
+ * per same-format run of q|k|v and gate|up, every other tensor cast to f16;
+ * read them with grout_model_qweights) in the fused layouts (qkv_proj = q|k|v rows, gate_up_proj =
  * gate|up rows, lm_head shared with embed_tokens when tied), bf16/f32/f64
  * cast to f16 through f32 with round-to-nearest-even on the GPU.  Replaces
  * the weight half of Qwen3Engine::load (src/model.rs:1508-1600) and
@@ -281,7 +289,13 @@ typedef struct {
 int grout_engine_create_q(const grout_qwen3_config* config, const grout_qwen3_qweights* weights,
                           int device, grout_engine** out);
 
+/* Device pointers of a model loaded from a GGUF file (GROUT_EINVAL for an
+ * fp16 checkpoint, whose weights grout_model_weights returns; and the other
+ * way round).  Valid until grout_model_free. */
+int grout_model_qweights(const grout_model* model, grout_qwen3_qweights* weights);
+
 /* Engine::load (src/api.rs:60-90): grout_model_load + grout_engine_create
+ * (grout_engine_create_q for a .gguf path)
  * with max_ctx (0 = max_position_embeddings); the engine owns the model and
  * frees it in grout_engine_destroy. */
 int grout_engine_load(const char* model_dir, int max_ctx, int device, grout_engine** out);

@@ -145,3 +145,38 @@ def test_qengine_argument_errors(gpu):
     spec2["layers"][0]["q_proj"] = (Q4, np.zeros((odd.q_dim, 384 // 256 * 144), np.uint8))
     with pytest.raises(ValueError, match="not a multiple of 256"):
         QuantWeights(odd, **spec2)
+
+
+@pytest.mark.parametrize("plan", ["q4km-tied", "mixed-untied", "f16-embed"])
+def test_gguf_load_vs_quantized_engine_and_oracle(gpu, tmp_path, plan):
+    """A GGUF file of the same weights (norms as F32, matrices as their ggml
+    blocks) loaded by grout_engine_load gives the engine built from the
+    blocks directly, bit for bit, and the oracle's logits."""
+    from gguf_util import gguf_bytes, qwen3_meta, qwen3_tensors
+    from grout_amd.model import Engine, QuantWeights
+
+    cfg = configs()["g2"]
+    spec, host, w64 = qutil.mixed_weights(cfg, PLANS[plan], 13, 0.05)
+    path = tmp_path / "qwen3.gguf"
+    path.write_bytes(gguf_bytes(qwen3_meta(cfg, eos=3, ctx=64), qwen3_tensors(cfg, spec)))
+    print(f"gguf {plan} {path.stat().st_size} bytes", flush=True)
+    loaded = Engine.load(str(path))
+    direct = Engine.from_quantized(cfg, QuantWeights(cfg, **spec), max_ctx=64)
+    orc = Q.Qwen3Oracle(cfg, host, 64, decode_w64=w64)
+    assert loaded.meta().max_ctx == 64 and loaded.meta().eos_token_ids == (3,)
+    prompt = np.random.default_rng(8).integers(0, cfg.vocab_size, 19)
+    try:
+        a, b = loaded.prefill(prompt).values, direct.prefill(prompt).values
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        ref, _ = orc.prefill(prompt, nthreads=8)
+        tol = check_logits(a, ref, f"gguf {plan} prefill")
+        tok = int(np.argmax(a))
+        for i in range(3):
+            a, b = loaded.decode(tok).values, direct.decode(tok).values
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+            ref, _ = orc.decode(tok, nthreads=8)
+            check_logits(a, ref, f"gguf {plan} decode {i}")
+            tok = int(np.argmax(a))
+    finally:
+        loaded.close()
+        direct.close()
