@@ -357,7 +357,7 @@ def bench_gemv(steps, warmup):
 
 
 def bench_qgemv(steps, warmup):
-    """The low-bit GEMVs (Q8_0 / Q4_K / Q6_K) on the Qwen3-4B decode shapes:
+    """The low-bit GEMVs (Q8_0 / Q4_K / Q5_K / Q6_K) on the Qwen3-4B decode shapes:
     random ggml payloads (block scales set to 0.01) repacked once, then timed
     over enough rotating copies that more than 600 MB of weights cycle (past
     the 256 MB Infinity Cache).  GB/s counts the repacked weight bytes read
@@ -371,7 +371,8 @@ def bench_qgemv(steps, warmup):
     H, I, QKV, Q, V = 2560, 9728, 6144, 4096, 151936
     shapes = {"qkv": (QKV, H, False), "o_proj": (H, Q, False), "gate_up_silu": (2 * I, H, True),
               "down": (H, I, False), "lm_head": (V, H, False)}
-    fmts = {"Q8_0": (8, 32, 34, 0), "Q4_K": (12, 256, 144, 0), "Q6_K": (14, 256, 210, 208)}
+    fmts = {"Q8_0": (8, 32, 34, 0), "Q4_K": (12, 256, 144, 0), "Q5_K": (13, 256, 176, 0),
+            "Q6_K": (14, 256, 210, 208)}
     P = lambda t: C.c_void_p(t.data_ptr())
     d_bytes = torch.tensor([0.01], dtype=torch.float16).view(torch.uint8).to(dev)
     out = {}
@@ -384,7 +385,7 @@ def bench_qgemv(steps, warmup):
             for c in range(copies):
                 raw = torch.randint(0, 256, (n * k // be, bb), dtype=torch.uint8, device=dev)
                 raw[:, d_off:d_off + 2] = d_bytes
-                if fmt == 12:
+                if fmt in (12, 13):
                     raw[:, 2:4] = d_bytes
                 w = torch.empty(nbytes, dtype=torch.uint8, device=dev)
                 call("grout_qweight_repack", fmt, P(raw), n, k, P(w), None)

@@ -471,8 +471,8 @@ int convert_f16(const grout_qwen3_config* c, const grout_qwen3_weights* w, Mat& 
 int check_part(const grout_wpart& p, int k, const char* what, int layer) {
   const char* lname = layer < 0 ? "" : " of layer ";
   GROUT_NEED(p.fmt == GROUT_WFMT_F16 || p.fmt == GROUT_WFMT_Q8_0 || p.fmt == GROUT_WFMT_Q4_K ||
-                 p.fmt == GROUT_WFMT_Q6_K,
-             GROUT_ENOTSUP, "%s%s%d: format %d is not f16, Q8_0, Q4_K or Q6_K", what, lname,
+                 p.fmt == GROUT_WFMT_Q5_K || p.fmt == GROUT_WFMT_Q6_K,
+             GROUT_ENOTSUP, "%s%s%d: format %d is not f16, Q8_0, Q4_K, Q5_K or Q6_K", what, lname,
              layer, p.fmt);
   GROUT_NEED(p.rows >= 1, GROUT_EINVAL, "%s%s%d: rows=%d", what, lname, layer, p.rows);
   GROUT_NEED(p.data != nullptr && aligned16(p.data), GROUT_EINVAL,
@@ -739,8 +739,10 @@ int grout_gemv_rms_norm_silu_mul(const void* W, const void* residual, const void
 size_t grout_qweight_bytes(int fmt, int n, int k) { return grout::qweight_bytes(fmt, n, k); }
 
 static int check_q(int fmt, int n, int k) {
-  GROUT_NEED(fmt == GROUT_WFMT_Q8_0 || fmt == GROUT_WFMT_Q4_K || fmt == GROUT_WFMT_Q6_K,
-             GROUT_ENOTSUP, "weight format %d: Q8_0 (8), Q4_K (12) or Q6_K (14) expected", fmt);
+  GROUT_NEED(fmt == GROUT_WFMT_Q8_0 || fmt == GROUT_WFMT_Q4_K || fmt == GROUT_WFMT_Q5_K ||
+                 fmt == GROUT_WFMT_Q6_K,
+             GROUT_ENOTSUP, "weight format %d: Q8_0 (8), Q4_K (12), Q5_K (13) or Q6_K (14) expected",
+             fmt);
   GROUT_NEED(grout::qweight_bytes(fmt, n, k) != 0, GROUT_EINVAL,
              "[%d][%d] of format %d: k must be a multiple of the block size and <= 16384", n, k,
              fmt);

@@ -9,7 +9,7 @@
 // vocab = token_embd rows, tied head when output.weight is absent), the
 // tensor names of map_engine_tensor_name (src/loader.rs:660-698) and the
 // per-type load policy of load_device_weight_gguf (src/loader.rs:340-379):
-// Q8_0 / Q4_K / Q6_K matrices in the decode layout, F16 / F32 / BF16
+// Q8_0 / Q4_K / Q5_K / Q6_K matrices in the decode layout, F16 / F32 / BF16
 // tensors as f16, the token embedding gathered from its blocks and reused as
 // the head when tied.  The file is mmapped; every tensor's type, shape and
 // byte range is validated before the device is touched.
@@ -76,6 +76,15 @@ const char* type_name(uint32_t t) {
     case kTQ4_K: return "Q4_K";
     case kTQ5_K: return "Q5_K";
     case kTQ6_K: return "Q6_K";
+    // types a GGUF file may hold that this loader does not read
+    case 2: return "Q4_0";
+    case 3: return "Q4_1";
+    case 6: return "Q5_0";
+    case 7: return "Q5_1";
+    case 9: return "Q8_1";
+    case 10: return "Q2_K";
+    case 11: return "Q3_K";
+    case 15: return "Q8_K";
     default: return "?";
   }
 }
@@ -430,6 +439,7 @@ int engine_fmt(uint32_t t) {
     case kTF32: case kTF16: case kTBF16: return GROUT_WFMT_F16;
     case kTQ8_0: return GROUT_WFMT_Q8_0;
     case kTQ4_K: return GROUT_WFMT_Q4_K;
+    case kTQ5_K: return GROUT_WFMT_Q5_K;
     case kTQ6_K: return GROUT_WFMT_Q6_K;
     default: return -1;
   }

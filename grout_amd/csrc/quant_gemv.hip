@@ -1,11 +1,11 @@
-// Low-bit decode GEMVs over ggml-quantized weights (Q8_0, Q4_K, Q6_K).
+// Low-bit decode GEMVs over ggml-quantized weights (Q8_0, Q4_K, Q5_K, Q6_K).
 //
-// Reference: gemv_q8_0_f16 / gemv_q4k_f16 / gemv_q6k_f16 and their SoA
-// variants (src/kernels.rs:259-428, 564-804) over the weights GGUF files hold
+// Reference: gemv_q8_0_f16 / gemv_q4k_f16 / gemv_q5k_f16 / gemv_q6k_f16 and
+// their SoA variants (src/kernels.rs:259-804) over the weights GGUF files hold
 // (dequantization rules: src/dequant.rs:211-335).  Same math: every weight
 // is dequantized in fp32 from its block (Q8_0: d*q; Q4_K: d*sc*q - dmin*m;
-// Q6_K: d*sc*(q-32)), multiplied by the fp16 input and accumulated in fp32;
-// the output row is rounded to f16.
+// Q5_K: the same with a fifth bit of q; Q6_K: d*sc*(q-32)), multiplied by the
+// fp16 input and accumulated in fp32; the output row is rounded to f16.
 //
 // GPU layout (grout_qweight_repack): the ggml blocks are split into aligned
 // arrays, bytes unchanged, so every dequantized value is the reference's and
@@ -13,6 +13,7 @@
 //   Q8_0: q  int8 [N][K]          d  f16 [N][K/32]
 //   Q4_K: q  u8   [N][K/2] (each superblock's 128 qs bytes in ggml order)
 //         h  16 B [N][K/256] (d, dmin, the 12 packed 6-bit scale/min bytes)
+//   Q5_K: q and h as Q4_K, qh u8 [N][K/8] (each superblock's 32 qh bytes)
 //   Q6_K: ql u8 [N][K/2], qh u8 [N][K/4], sc int8 [N][K/16], d f16 [N][K/256]
 //
 // GEMV kernel: one 16-lane team per weight row, x and the rows' decoded
@@ -44,9 +45,10 @@ __host__ __device__ inline QLayout qlayout(int fmt, size_t n, size_t k) {
   if (fmt == 8) {
     sz[0] = n * k;
     sz[1] = n * (k / 32) * 2;
-  } else if (fmt == 12) {
+  } else if (fmt == 12 || fmt == 13) {
     sz[0] = n * k / 2;
     sz[1] = n * (k / 256) * 16;
+    if (fmt == 13) sz[2] = n * k / 8;
   } else if (fmt == 14) {
     sz[0] = n * k / 2;
     sz[1] = n * k / 4;
@@ -84,6 +86,15 @@ __global__ __launch_bounds__(256) void qrepack_kernel(int fmt, const uint8_t* __
     for (int i = 0; i < 128; ++i) q[i] = s[16 + i];
     uint8_t* h = dst + L.off[1] + (row * blocks_per_row + j) * 16;
     for (int i = 0; i < 16; ++i) h[i] = s[i];
+  } else if (fmt == 13) {
+    // d, dmin, scales[12] at 0, qh[32] at 16, qs[128] at 48
+    const uint8_t* s = src + b * 176;
+    uint8_t* q = dst + L.off[0] + row * (k / 2) + j * 128;
+    for (int i = 0; i < 128; ++i) q[i] = s[48 + i];
+    uint8_t* h = dst + L.off[1] + (row * blocks_per_row + j) * 16;
+    for (int i = 0; i < 16; ++i) h[i] = s[i];
+    uint8_t* qh = dst + L.off[2] + row * (k / 8) + j * 32;
+    for (int i = 0; i < 32; ++i) qh[i] = s[16 + i];
   } else {
     const uint8_t* s = src + b * 210;
     uint8_t* ql = dst + L.off[0] + row * (k / 2) + j * 128;
@@ -103,7 +114,8 @@ __global__ __launch_bounds__(256) void qrepack_kernel(int fmt, const uint8_t* __
 // A row team of 16 lanes owns one weight row; lane m takes the row's pieces
 // p = m, m + 16, ... (a piece is 32 consecutive weights: Q8_0 one block;
 // Q4_K 16 qs bytes = 16 weights of sub-block 2g in the low nibbles and 16 of
-// 2g+1 in the high; Q6_K 16 ql bytes and the 16 qh bytes they pair with), so a
+// 2g+1 in the high; Q5_K the same and the 16 qh bytes holding their fifth
+// bits; Q6_K 16 ql bytes and the 16 qh bytes they pair with), so a
 // team reads 256 contiguous bytes per load and p % 8 == m % 8 fixes each
 // lane's place inside a superblock.  Workgroups of R teams (4 for short
 // matrices so the grid covers every CU, 16 for tall ones); before the
@@ -133,12 +145,12 @@ __device__ __forceinline__ half_t f2h_signed(float p) {
 // blind to bits 6 and up: xswz(G + 64 i) = xswz(G) + 64 i.
 template <int FMT>
 __host__ __device__ constexpr int xswz(int G) {
-  return FMT == 8    ? G ^ ((G >> 3) & 3) ^ (((G >> 5) & 1) << 3)
-         : FMT == 12 ? G ^ ((G >> 3) & 1) ^ (((G >> 4) & 1) << 2) ^ (((G >> 5) & 1) << 3)
-                     : G ^ ((G >> 4) & 1) ^ (((G >> 5) & 1) << 3);
+  return FMT == 8                  ? G ^ ((G >> 3) & 3) ^ (((G >> 5) & 1) << 3)
+         : FMT == 12 || FMT == 13 ? G ^ ((G >> 3) & 1) ^ (((G >> 4) & 1) << 2) ^ (((G >> 5) & 1) << 3)
+                                  : G ^ ((G >> 4) & 1) ^ (((G >> 5) & 1) << 3);
 }
 
-// Slot of 16-run r in the Q4_K x sums (runs r and r + 2 of one piece side by
+// Slot of 16-run r in the Q4_K and Q5_K x sums (runs r and r + 2 of one piece side by
 // side) and in the Q6_K scales and x sums (runs r and r + 4 side by side).
 __host__ __device__ constexpr int xsum_slot(int r) { return (r & ~3) | ((r & 1) << 1) | ((r >> 1) & 1); }
 __host__ __device__ constexpr int q6_slot(int r) { return (r & ~7) | ((r & 3) << 1) | ((r >> 2) & 1); }
@@ -159,8 +171,8 @@ __device__ __forceinline__ int qrow(int lr, int N, int& out) {
 
 // Raw bytes of one piece.
 struct QPc {
-  u32x4 a;  // Q8_0 q[0..15]; Q4_K qs; Q6_K ql
-  u32x4 b;  // Q8_0 q[16..31]; Q6_K qh
+  u32x4 a;  // Q8_0 q[0..15]; Q4_K, Q5_K qs; Q6_K ql
+  u32x4 b;  // Q8_0 q[16..31]; Q5_K, Q6_K qh
 };
 
 template <int FMT>
@@ -174,6 +186,10 @@ __device__ __forceinline__ QPc qpc_load(const uint8_t* __restrict__ W, const QLa
   } else if (FMT == 12) {
     r.a = load_stream16(W + L.off[0] + (size_t)row * (K / 2) + (size_t)p * 16);
     r.b = r.a;
+  } else if (FMT == 13) {
+    r.a = load_stream16(W + L.off[0] + (size_t)row * (K / 2) + (size_t)p * 16);
+    // qh bytes 16 l0 .. +15 of superblock p / 8 (l0 = bit 0 of p)
+    r.b = load_stream16(W + L.off[2] + (size_t)row * (K / 8) + (size_t)(p >> 3) * 32 + (p & 1) * 16);
   } else {
     r.a = load_stream16(W + L.off[0] + (size_t)row * (K / 2) + (size_t)p * 16);
     // qh bytes 32n + 16 l0 .. +15 of superblock p / 8 (n = bit 2 of p, l0 = bit 0)
@@ -205,7 +221,7 @@ __device__ __forceinline__ float ddot16(const uint32_t (&w)[4], half8 x0, half8 
 }
 
 // Per-lane LDS offsets for piece i = 0 (piece i adds 64 i granules, and 16 i
-// (Q8_0) or 32 i (Q4_K, Q6_K) floats of scales and x sums).
+// (Q8_0) or 32 i (Q4_K, Q5_K, Q6_K) floats of scales and x sums).
 struct QLane {
   int xg[4];  // byte offsets of the x granules: Q8_0 4 of one run; else lo, lo+1, hi, hi+1
   int so;     // float offset into the row's scales
@@ -219,7 +235,7 @@ __device__ __forceinline__ QLane qlane(int m) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) q.xg[k] = 16 * xswz<FMT>(4 * m + k);
     q.so = q.xo = m;
-  } else if (FMT == 12) {
+  } else if (FMT == 12 || FMT == 13) {
     // lo run: weights 256 sb + 64 g + 16 l0 (sub-block 2g), hi run +32 (2g+1)
     const int g = (m >> 1) & 3, l0 = m & 1, s3 = m >> 3;
     const int G = 32 * s3 + 8 * g + 2 * l0;
@@ -276,6 +292,22 @@ __device__ __forceinline__ float qpc_dot(const QPc& r, int m, const QLane& q,
     const floatx4 sc = *reinterpret_cast<const floatx4*>(s_row + q.so + 32 * I);
     const float2 xs = *reinterpret_cast<const float2*>(s_xsum + q.xo + 32 * I);
     return (sc[0] * dlo - sc[1] * xs.x) + (sc[2] * dhi - sc[3] * xs.y);
+  } else if (FMT == 13) {
+    // fifth bits: bit 2g of qh byte l for the lo run, bit 2g + 1 for the hi
+    const int g = (m >> 1) & 3;
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t t = r.b[i] >> (2 * g);
+      lo[i] = (r.a[i] & 0x0F0F0F0Fu) | ((t << 4) & 0x10101010u);
+      hi[i] = ((r.a[i] >> 4) & 0x0F0F0F0Fu) | ((t << 3) & 0x10101010u);
+    }
+    const float dlo = ddot16(lo, xgran<I>(s_xb, q.xg[0]), xgran<I>(s_xb, q.xg[1]), 0.f);
+    const float dhi = ddot16(hi, xgran<I>(s_xb, q.xg[2]), xgran<I>(s_xb, q.xg[3]), 0.f);
+    // {2^24 d sc_2g, dmin m_2g, 2^24 d sc_2g+1, dmin m_2g+1}
+    const floatx4 sc = *reinterpret_cast<const floatx4*>(s_row + q.so + 32 * I);
+    const float2 xs = *reinterpret_cast<const float2*>(s_xsum + q.xo + 32 * I);
+    return (sc[0] * dlo - sc[1] * xs.x) + (sc[2] * dhi - sc[3] * xs.y);
   } else {
     // 6-bit q held + 32: sum (q + 32) x - 32 sum x per run
     const int ilo = (m >> 1) & 1;
@@ -294,7 +326,7 @@ __device__ __forceinline__ float qpc_dot(const QPc& r, int m, const QLane& q,
 }
 
 // Staging of x: granule c to its swizzled slot, and the x sum of each run
-// (Q8_0: 32-runs = granules c..c+3, scaled by 128 * 2^-24; Q4_K: 16-runs;
+// (Q8_0: 32-runs = granules c..c+3, scaled by 128 * 2^-24; Q4_K, Q5_K: 16-runs;
 // Q6_K: 16-runs scaled by 32 * 2^-24), the run's granules sitting in
 // adjacent lanes.  Every lane calls it.
 template <int FMT>
@@ -308,7 +340,7 @@ __device__ __forceinline__ void stage_x(u32x4 v, int c, int NG, half_t* s_x, flo
   if (FMT == 8) {
     s += __shfl_xor(s, 2, 64);
     if (c < NG && (c & 3) == 0) s_xsum[c >> 2] = s * 0x1p-17f;
-  } else if (FMT == 12) {
+  } else if (FMT == 12 || FMT == 13) {
     if (c < NG && (c & 1) == 0) s_xsum[xsum_slot(c >> 1)] = s;
   } else {
     if (c < NG && (c & 1) == 0) s_xsum[q6_slot(c >> 1)] = s * 0x1p-19f;
@@ -316,7 +348,7 @@ __device__ __forceinline__ void stage_x(u32x4 v, int c, int NG, half_t* s_x, flo
   if (c < NG) *reinterpret_cast<u32x4*>(s_x + 8 * xswz<FMT>(c)) = v;
 }
 
-// One staging unit: Q8_0 one block scale; Q4_K one superblock header; Q6_K
+// One staging unit: Q8_0 one block scale; Q4_K, Q5_K one superblock header; Q6_K
 // one superblock's 16 scales and d.
 struct SRaw {
   u32x4 v;
@@ -334,7 +366,7 @@ __device__ __forceinline__ SRaw stage_load(const uint8_t* __restrict__ W, const 
   s.d = 0;
   if (FMT == 8) {
     s.d = *reinterpret_cast<const uint16_t*>(W + L.off[1] + ((size_t)row * (K / 32) + k) * 2);
-  } else if (FMT == 12) {
+  } else if (FMT == 12 || FMT == 13) {
     s.v = load16(W + L.off[1] + ((size_t)row * (K / 256) + k) * 16);
   } else {
     s.v = load16(W + L.off[2] + (size_t)row * (K / 16) + (size_t)k * 16);
@@ -344,8 +376,9 @@ __device__ __forceinline__ SRaw stage_load(const uint8_t* __restrict__ W, const 
 }
 
 // Scales as the reference's decode layout holds them (Q8_0 d; Q6_K d * sc in
-// fp32; Q4_K the effective f16(d * sc) and f16(dmin * m)), times the power of
-// two that undoes the denormal encoding (exact).
+// fp32; Q4_K the effective f16(d * sc) and f16(dmin * m); Q5_K, read in the
+// native layout, d * sc and dmin * m in fp32), times the power of two that
+// undoes the denormal encoding (exact).
 template <int FMT>
 __device__ __forceinline__ void stage_store(const SRaw& s, int u, int U, int UPR, int SCW,
                                             float* s_sc) {
@@ -354,7 +387,7 @@ __device__ __forceinline__ void stage_store(const SRaw& s, int u, int U, int UPR
   float* dst = s_sc + lr * SCW;
   if (FMT == 8) {
     dst[k] = h2f_bits((uint16_t)s.d) * 0x1p24f;
-  } else if (FMT == 12) {
+  } else if (FMT == 12 || FMT == 13) {
     // d, dmin, then eight 6-bit (scale, min) pairs packed in 12 bytes
     const float d = h2f_bits((uint16_t)(s.v[0] & 0xFFFFu));
     const float dmin = h2f_bits((uint16_t)(s.v[0] >> 16));
@@ -372,13 +405,21 @@ __device__ __forceinline__ void stage_store(const SRaw& s, int u, int U, int UPR
         mn[j] = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
       }
     }
+    if (FMT == 12) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
-      *reinterpret_cast<floatx4*>(dst + 16 * k + 4 * g) =
-          floatx4{(float)f2h_signed(d * (float)sc[2 * g]) * 0x1p24f,
-                  (float)f2h_signed(dmin * (float)mn[2 * g]),
-                  (float)f2h_signed(d * (float)sc[2 * g + 1]) * 0x1p20f,
-                  (float)f2h_signed(dmin * (float)mn[2 * g + 1])};
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<floatx4*>(dst + 16 * k + 4 * g) =
+            floatx4{(float)f2h_signed(d * (float)sc[2 * g]) * 0x1p24f,
+                    (float)f2h_signed(dmin * (float)mn[2 * g]),
+                    (float)f2h_signed(d * (float)sc[2 * g + 1]) * 0x1p20f,
+                    (float)f2h_signed(dmin * (float)mn[2 * g + 1])};
+    } else {  // the products are exact in fp32 (11-bit d times a 6-bit integer)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<floatx4*>(dst + 16 * k + 4 * g) =
+            floatx4{(d * (float)sc[2 * g]) * 0x1p24f, dmin * (float)mn[2 * g],
+                    (d * (float)sc[2 * g + 1]) * 0x1p24f, dmin * (float)mn[2 * g + 1]};
+    }
   } else {
     const float d = h2f_bits((uint16_t)s.d);
     float f[16];
@@ -623,8 +664,8 @@ __global__ __launch_bounds__(R * S * kQTeam) void gemv_q_kernel(const uint8_t* _
 
 // Raw bytes of one piece (row, j).
 struct QRaw {
-  u32x4 a;  // primary payload: Q8_0 q, Q4_K q, Q6_K ql
-  u32x4 b;  // Q6_K: the 16 qh bytes of the piece's runs
+  u32x4 a;  // primary payload: Q8_0 q, Q4_K and Q5_K qs, Q6_K ql
+  u32x4 b;  // Q5_K, Q6_K: the 16 qh bytes of the piece's runs
 };
 
 template <int FMT>
@@ -635,6 +676,9 @@ __device__ __forceinline__ QRaw qload(const uint8_t* __restrict__ W, const QLayo
     r.a = load_stream16(W + L.off[0] + (size_t)row * K + (size_t)j * 16);
   } else if (FMT == 12) {
     r.a = load_stream16(W + L.off[0] + (size_t)row * (K / 2) + (size_t)j * 16);
+  } else if (FMT == 13) {
+    r.a = load_stream16(W + L.off[0] + (size_t)row * (K / 2) + (size_t)j * 16);
+    r.b = load_stream16(W + L.off[2] + (size_t)row * (K / 8) + (size_t)(j >> 3) * 32 + (j & 1) * 16);
   } else {
     r.a = load_stream16(W + L.off[0] + (size_t)row * (K / 2) + (size_t)j * 16);
     const int sb = j >> 3, o = (j & 7) * 16, n = o >> 6, h = o & 63;
@@ -650,6 +694,7 @@ __device__ __forceinline__ QRaw qload(const uint8_t* __restrict__ W, const QLayo
 // once to f16.  DECODE: the decode layout's Q4_K scales, f16(d * sc) and
 // f16(dmin * m); otherwise the CPU rule, d * sc and dmin * m in fp32 (the
 // reference's native-layout embedding gather, src/kernels.rs:1963-2007).
+// Q5_K has only the CPU rule (the reference keeps it in the native layout).
 template <int FMT, bool DECODE>
 __device__ __forceinline__ void dequant_piece(const uint8_t* __restrict__ W, const QLayout& L,
                                               int row, int j, int K, half_t* __restrict__ o) {
@@ -660,7 +705,7 @@ __device__ __forceinline__ void dequant_piece(const uint8_t* __restrict__ W, con
                                                                  ((size_t)row * (K / 32) + (j >> 1)) * 2));
     const int8_t* q = reinterpret_cast<const int8_t*>(&r.a);
     for (int i = 0; i < 16; ++i) o[16 * j + i] = f2h_signed((float)q[i] * d);
-  } else if (FMT == 12) {
+  } else if (FMT == 12 || FMT == 13) {
     const int sb = j >> 3, g = (j & 7) >> 1, l0 = (j & 1) * 16;
     const uint8_t* hb = W + L.off[1] + ((size_t)row * (K / 256) + sb) * 16;
     const float d = h2f_bits((uint16_t)(hb[0] | (hb[1] << 8)));
@@ -679,7 +724,7 @@ __device__ __forceinline__ void dequant_piece(const uint8_t* __restrict__ W, con
     }
     float d1 = d * (float)s[0], m1 = dmin * (float)m[0];
     float d2 = d * (float)s[1], m2 = dmin * (float)m[1];
-    if (DECODE) {  // effective scales of the decode layout
+    if (DECODE && FMT == 12) {  // effective scales of the decode layout
       d1 = (float)f2h_signed(d1);
       m1 = (float)f2h_signed(m1);
       d2 = (float)f2h_signed(d2);
@@ -687,9 +732,12 @@ __device__ __forceinline__ void dequant_piece(const uint8_t* __restrict__ W, con
     }
     const uint8_t* q = reinterpret_cast<const uint8_t*>(&r.a);
     const int e0 = sb * 256 + 64 * g + l0;
+    const uint8_t* qh = reinterpret_cast<const uint8_t*>(&r.b);
     for (int i = 0; i < 16; ++i) {
-      o[e0 + i] = f2h_signed(d1 * (float)(q[i] & 0xF) - m1);
-      o[e0 + 32 + i] = f2h_signed(d2 * (float)(q[i] >> 4) - m2);
+      const int hlo = FMT == 13 ? ((qh[i] >> (2 * g)) & 1) << 4 : 0;
+      const int hhi = FMT == 13 ? ((qh[i] >> (2 * g + 1)) & 1) << 4 : 0;
+      o[e0 + i] = f2h_signed(d1 * (float)((q[i] & 0xF) + hlo) - m1);
+      o[e0 + 32 + i] = f2h_signed(d2 * (float)((q[i] >> 4) + hhi) - m2);
     }
   } else {
     const int sb = j >> 3, o16 = (j & 7) * 16, n = o16 >> 6, h = o16 & 63;
@@ -742,7 +790,7 @@ __global__ __launch_bounds__(256) void qgather_kernel(const uint8_t* __restrict_
 static bool qfmt_ok(int fmt, int N, int K) {
   if (N < 1 || K < 1) return false;
   const int blk = fmt == 8 ? 32 : 256;
-  if (fmt != 8 && fmt != 12 && fmt != 14) return false;
+  if (fmt != 8 && fmt != 12 && fmt != 13 && fmt != 14) return false;
   return K % blk == 0 && K <= kQMaxK;
 }
 
@@ -862,6 +910,10 @@ hipError_t launch_gemv_q_norm(int fmt, const void* W, const void* residual, cons
       if (norm) gemv_q_launch<12, true>(W, x, y, N, K, silu, nz, stream);
       else gemv_q_launch<12, false>(W, x, y, N, K, silu, nz, stream);
       break;
+    case 13:
+      if (norm) gemv_q_launch<13, true>(W, x, y, N, K, silu, nz, stream);
+      else gemv_q_launch<13, false>(W, x, y, N, K, silu, nz, stream);
+      break;
     default:
       if (norm) gemv_q_launch<14, true>(W, x, y, N, K, silu, nz, stream);
       else gemv_q_launch<14, false>(W, x, y, N, K, silu, nz, stream);
@@ -880,6 +932,7 @@ hipError_t launch_qgather(int fmt, const void* W, int N, int K, const uint32_t* 
   switch (fmt) {
     case 8: qgather_kernel<8><<<blocks, 256, 0, stream>>>(w, N, K, L, ids, rows, (half_t*)out); break;
     case 12: qgather_kernel<12><<<blocks, 256, 0, stream>>>(w, N, K, L, ids, rows, (half_t*)out); break;
+    case 13: qgather_kernel<13><<<blocks, 256, 0, stream>>>(w, N, K, L, ids, rows, (half_t*)out); break;
     default: qgather_kernel<14><<<blocks, 256, 0, stream>>>(w, N, K, L, ids, rows, (half_t*)out); break;
   }
   return hipGetLastError();
@@ -894,6 +947,7 @@ hipError_t launch_qweight_dequant(int fmt, const void* W, int N, int K, void* ou
   switch (fmt) {
     case 8: qdequant_kernel<8><<<blocks, 256, 0, stream>>>((const uint8_t*)W, N, K, L, (half_t*)out); break;
     case 12: qdequant_kernel<12><<<blocks, 256, 0, stream>>>((const uint8_t*)W, N, K, L, (half_t*)out); break;
+    case 13: qdequant_kernel<13><<<blocks, 256, 0, stream>>>((const uint8_t*)W, N, K, L, (half_t*)out); break;
     default: qdequant_kernel<14><<<blocks, 256, 0, stream>>>((const uint8_t*)W, N, K, L, (half_t*)out); break;
   }
   return hipGetLastError();

@@ -149,8 +149,9 @@ class Qwen3Weights:
 
 
 # Weight formats (ggml type ids for the low-bit ones; include/grout_engine.h).
-F16, Q8_0, Q4_K, Q6_K = 0, 8, 12, 14
-QBLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}  # (weights, bytes) per block
+F16, Q8_0, Q4_K, Q5_K, Q6_K = 0, 8, 12, 13, 14
+QBLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176),
+          Q6_K: (256, 210)}  # (weights, bytes) per block
 QLAYER_VECS = ("input_layernorm", "q_norm", "k_norm", "post_attention_layernorm")
 QLAYER_MATS = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
 
@@ -161,7 +162,7 @@ class QuantWeights:
     src/weights.rs:7-56).
 
     Every matrix is (fmt, data): fmt F16 with data an fp16 [rows][k] array
-    (numpy fp16 or uint16 bit patterns), or Q8_0 / Q4_K / Q6_K with data the
+    (numpy fp16 or uint16 bit patterns), or Q8_0 / Q4_K / Q5_K / Q6_K with data the
     tensor's ggml blocks (uint8, rows contiguous).  q|k|v and gate|up runs of
     one low-bit format are concatenated and repacked as one part (one GEMV in
     the decode step); a format change starts a new part.  The norm vectors
@@ -272,6 +273,10 @@ class QuantWeights:
             d = std / (32.0 * 4.6)
             b[:, 0:2] = f16(d)
             b[:, 2:4] = f16(7.5 * d)
+        elif fmt == Q5_K:    # q uniform 0..31: centred by dmin = 15.5 d
+            d = std / (32.0 * 9.2)
+            b[:, 0:2] = f16(d)
+            b[:, 2:4] = f16(15.5 * d)
         else:                # Q6_K: (q - 32) std ~18.5, int8 scales |sc| ~64
             b[:, 208:210] = f16(std / (74.0 * 18.5))
         return b.reshape(rows, -1)

@@ -124,6 +124,7 @@ int grout_gemv_rms_norm_silu_mul(const void* W, const void* residual, const void
 #define GROUT_WFMT_F16 0    /* plain fp16 [n][k] */
 #define GROUT_WFMT_Q8_0 8   /* ggml type ids */
 #define GROUT_WFMT_Q4_K 12
+#define GROUT_WFMT_Q5_K 13
 #define GROUT_WFMT_Q6_K 14
 
 /* Device bytes of an [n][k] matrix of format fmt in the GEMV layout (0 when
@@ -137,8 +138,8 @@ int grout_qweight_repack(int fmt, const void* ggml_blocks, int n, int k, void* o
                          void* stream);
 
 /* y[r] = f16(sum_k dequant(W)[r][k] x[k]), fp32 dequantization and
- * accumulation.  Replaces gemv_q8_0_f16 / gemv_q4k_f16 / gemv_q6k_f16 and
- * their SoA forms (src/kernels.rs:259-428, 564-804). */
+ * accumulation.  Replaces gemv_q8_0_f16 / gemv_q4k_f16 / gemv_q5k_f16 /
+ * gemv_q6k_f16 and their SoA forms (src/kernels.rs:259-804). */
 int grout_gemv_q(int fmt, const void* wq, const void* x, void* y, int n, int k, void* stream);
 
 /* wq holds 2*inter rows [gate | up]: y[i] = f16(silu(g_i) * u_i) with g_i,
@@ -164,15 +165,16 @@ int grout_gemv_q_rms_norm_silu_mul(int fmt, const void* wq, const void* residual
 
 /* The [n][k] matrix dequantized to f16 (out) with the decode layout's scales,
  * e.g. for prefill GEMMs: the reference's prefill dequant into its pooled
- * scratch (dequant_q4k_soa_to_f16 / dequant_q6k_soa_to_f16 /
- * dequant_q8_0_to_f16, src/kernels.rs:1075-1160; src/quant_scratch.rs). */
+ * scratch (dequant_q4k_soa_to_f16 / dequant_q5k_to_f16 /
+ * dequant_q6k_soa_to_f16 / dequant_q8_0_to_f16, src/kernels.rs:1075-1300;
+ * src/quant_scratch.rs). */
 int grout_qweight_dequant(int fmt, const void* wq, int n, int k, void* out, void* stream);
 
 /* out[t][0..k) = row ids[t] of the [n][k] matrix as f16 for t < rows, by the
  * CPU dequantization rule (Q4_K with fp32 d*sc and dmin*m); ids (device
  * memory) at or past n read row n - 1.  The token-embedding gather from a
  * quantized table: embed_gather_q8_0_f16 / embed_gather_q4k_f16 /
- * embed_gather_q6k_f16 (src/kernels.rs:1940-2060). */
+ * embed_gather_q5k_f16 / embed_gather_q6k_f16 (src/kernels.rs:1940-2120). */
 int grout_qweight_gather(int fmt, const void* wq, int n, int k, const uint32_t* ids, int rows,
                          void* out, void* stream);
 
@@ -217,7 +219,7 @@ typedef struct grout_model grout_model;
  * instead: the qwen3.* metadata becomes the config (config_from_gguf,
  * src/loader.rs:276-330), eos = tokenizer.ggml.eos_token_id, the head is tied
  * when output.weight is absent, and every tensor must be F32/F16/BF16 (norms)
- * or F32/F16/BF16/Q8_0/Q4_K/Q6_K (matrices) with the config's shape; the
+ * or F32/F16/BF16/Q8_0/Q4_K/Q5_K/Q6_K (matrices) with the config's shape; the
  * reader's bounds are the reference's (src/gguf.rs:212-445).  weight_bytes is
  * then the device bytes in the low-bit layouts. */
 int grout_model_inspect(const char* model_dir, grout_model_info* info);
@@ -247,7 +249,7 @@ int grout_engine_create(const grout_qwen3_config* config, const grout_qwen3_weig
 
 /* One weight matrix of a projection: `rows` output rows over the
  * projection's input width k, as f16 [rows][k] (fmt GROUT_WFMT_F16) or in
- * grout_qweight_repack's layout (GROUT_WFMT_Q8_0 / Q4_K / Q6_K).  Mirrors
+ * grout_qweight_repack's layout (GROUT_WFMT_Q8_0 / Q4_K / Q5_K / Q6_K).  Mirrors
  * Weight / MatrixWeight (src/weights.rs:7-56), whose parts may differ in
  * format (a Q4_K_M file stores some attn_v and ffn_down matrices as Q6_K). */
 typedef struct {

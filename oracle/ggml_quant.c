@@ -13,6 +13,10 @@
  *         group g (64 weights) = bytes qs[32g .. 32g+31]: low nibble of byte l
  *         is weight 64g+l (sub-block 2g), high nibble weight 64g+32+l
  *         (sub-block 2g+1);                                    w = d*sc*q - dmin*m
+ *   Q5_K 176 B per 256 weights: f16 d, dmin; u8 scales[12]; u8 qh[32]; u8 qs[128]
+ *         as Q4_K with a fifth bit: weight 64g + l (+32) takes bit 2g (2g+1)
+ *         of qh[l] as 16;                                   w = d*sc*q - dmin*m
+ *         (src/dequant.rs:255-294)
  *   Q6_K 210 B per 256 weights: u8 ql[128]; u8 qh[64]; int8 sc[16]; f16 d
  *         half n (128 weights), l < 32: 6-bit q = ql nibble | 2 bits of qh,
  *         weights 128n + l + 32i (i = 0..3) use
@@ -43,7 +47,7 @@
 float go_h2f(uint16_t h);
 uint16_t go_f2h(float f);
 
-enum { GQ_Q8_0 = 8, GQ_Q4_K = 12, GQ_Q6_K = 14 };
+enum { GQ_Q8_0 = 8, GQ_Q4_K = 12, GQ_Q5_K = 13, GQ_Q6_K = 14 };
 
 static uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
 
@@ -59,7 +63,7 @@ static void scale_min_k4(int j, const uint8_t* q, int* sc, int* m) {
 }
 
 int go_qblock_bytes(int fmt) {
-  return fmt == GQ_Q8_0 ? 34 : fmt == GQ_Q4_K ? 144 : fmt == GQ_Q6_K ? 210 : -1;
+  return fmt == GQ_Q8_0 ? 34 : fmt == GQ_Q4_K ? 144 : fmt == GQ_Q5_K ? 176 : fmt == GQ_Q6_K ? 210 : -1;
 }
 int go_qblock_elems(int fmt) { return fmt == GQ_Q8_0 ? 32 : 256; }
 
@@ -95,6 +99,24 @@ static int dequant_mode(int fmt, const uint8_t* blocks, size_t n, float* out, in
         for (int l = 0; l < 32; ++l) {
           y[64 * g + l] = d1 * (float)(qs[32 * g + l] & 0xF) - m1;
           y[64 * g + 32 + l] = d2 * (float)(qs[32 * g + l] >> 4) - m2;
+        }
+      }
+    } else if (fmt == GQ_Q5_K) { /* src/dequant.rs:255-294 (both modes: scales as stored) */
+      const float d = go_h2f(rd16(x)), dmin = go_h2f(rd16(x + 2));
+      const uint8_t* scales = x + 4;
+      const uint8_t* qh = x + 16;
+      const uint8_t* qs = x + 48;
+      for (int g = 0; g < 4; ++g) {
+        int sc, m;
+        scale_min_k4(2 * g, scales, &sc, &m);
+        const float d1 = d * (float)sc, m1 = dmin * (float)m;
+        scale_min_k4(2 * g + 1, scales, &sc, &m);
+        const float d2 = d * (float)sc, m2 = dmin * (float)m;
+        for (int l = 0; l < 32; ++l) {
+          const int q1 = (qs[32 * g + l] & 0xF) + ((qh[l] >> (2 * g)) & 1) * 16;
+          const int q2 = (qs[32 * g + l] >> 4) + ((qh[l] >> (2 * g + 1)) & 1) * 16;
+          y[64 * g + l] = d1 * (float)q1 - m1;
+          y[64 * g + 32 + l] = d2 * (float)q2 - m2;
         }
       }
     } else { /* Q6_K, src/dequant.rs:296-323 */

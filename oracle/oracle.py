@@ -13,7 +13,7 @@ __all__ = [
     "splitmix64_at", "inv_freq", "rope_table", "rsqrt_det", "sumsq_row128",
     "qk_norm_rope_row", "qk_norm_rope_kv_prefill", "qk_norm_rope_kv_decode",
     "attention_prefill_rows", "attention_decode", "decode_split", "splitk_merge",
-    "Q8_0", "Q4_K", "Q6_K", "qblock", "dequant", "gemv_q",
+    "Q8_0", "Q4_K", "Q5_K", "Q6_K", "qblock", "dequant", "gemv_q",
     "SEED_BASE", "seed_for",
 ]
 
@@ -218,7 +218,7 @@ def decode_split(q, k_cache, v_cache, pos: int, BN: int, NKS: int, scale=None):
     return att, lse
 
 
-Q8_0, Q4_K, Q6_K = 8, 12, 14  # ggml type ids
+Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14  # ggml type ids
 
 
 def qblock(fmt: int):

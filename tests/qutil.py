@@ -1,5 +1,5 @@
 """Low-bit weight helpers for the tests: ggml block quantizers (float
-weights -> Q8_0 / Q4_K / Q6_K blocks, written from the published block
+weights -> Q8_0 / Q4_K / Q5_K / Q6_K blocks, written from the published block
 layouts, the inverse of oracle/ggml_quant.c's decoding; scale choices are
 simple absmax / min-max ones, not llama.cpp's search) and a builder of
 mixed-format Qwen3 weights for grout_engine_create_q together with the
@@ -51,10 +51,11 @@ def quantize(fmt: int, w: np.ndarray) -> np.ndarray:
         out[..., 192:208] = sc.view(np.uint8)
         out[..., 208:210] = d.view(np.uint8).reshape(rows, nb, 2)
         return out.reshape(rows, -1)
-    if fmt == O.Q4_K:
+    if fmt in (O.Q4_K, O.Q5_K):
+        qmax = 15 if fmt == O.Q4_K else 31
         b = w.reshape(rows, nb, 8, 32)  # 8 sub-blocks of 32 weights
         lo = np.minimum(b.min(-1), 0)
-        scale = (b.max(-1) - lo) / f32(15)
+        scale = (b.max(-1) - lo) / f32(qmax)
         mn = -lo
         d = (scale.max(-1) / f32(63)).astype(np.float16)
         dmin = (mn.max(-1) / f32(63)).astype(np.float16)
@@ -62,18 +63,26 @@ def quantize(fmt: int, w: np.ndarray) -> np.ndarray:
         sc = np.clip(np.rint(scale / _safe(df)[..., None]), 0, 63).astype(np.int64)
         m = np.clip(np.rint(mn / _safe(dmf)[..., None]), 0, 63).astype(np.int64)
         es, em = df[..., None] * sc.astype(f32), dmf[..., None] * m.astype(f32)
-        q = np.clip(np.rint((b + em[..., None]) / _safe(es)[..., None]), 0, 15)
+        q = np.clip(np.rint((b + em[..., None]) / _safe(es)[..., None]), 0, qmax)
         q = np.where(es[..., None] > 0, q, 0).astype(np.uint8).reshape(rows, nb, 4, 2, 32)
         pk = np.zeros((rows, nb, 12), np.uint8)
         for j in range(4):  # 6-bit (scale, min) pairs in 12 bytes (get_scale_min_k4's inverse)
             pk[..., j] = (sc[..., j] & 63) | ((sc[..., j + 4] >> 4) << 6)
             pk[..., j + 4] = (m[..., j] & 63) | ((m[..., j + 4] >> 4) << 6)
             pk[..., j + 8] = (sc[..., j + 4] & 0xF) | ((m[..., j + 4] & 0xF) << 4)
-        out = np.zeros((rows, nb, 144), np.uint8)
+        out = np.zeros((rows, nb, 144 if fmt == O.Q4_K else 176), np.uint8)
         out[..., 0:2] = d.view(np.uint8).reshape(rows, nb, 2)
         out[..., 2:4] = dmin.view(np.uint8).reshape(rows, nb, 2)
         out[..., 4:16] = pk
-        out[..., 16:] = (q[..., 0, :] | (q[..., 1, :] << 4)).reshape(rows, nb, 128)
+        qs = ((q[..., 0, :] & 0xF) | ((q[..., 1, :] & 0xF) << 4)).reshape(rows, nb, 128)
+        if fmt == O.Q4_K:
+            out[..., 16:] = qs
+        else:  # fifth bits: weight 64 g + l (+32) -> bit 2 g (2 g + 1) of qh[l]
+            qh = np.zeros((rows, nb, 32), np.uint8)
+            for g in range(4):
+                qh |= ((q[..., g, 0, :] >> 4) << (2 * g)) | ((q[..., g, 1, :] >> 4) << (2 * g + 1))
+            out[..., 16:48] = qh
+            out[..., 48:] = qs
         return out.reshape(rows, -1)
     raise ValueError(f"format {fmt}")
 

@@ -10,10 +10,11 @@ import pytest
 
 import oracle as O
 import qutil
-from gguf_util import (ARRAY, F32, I32, STRING, T_Q5_K, U8, U32, U64, gguf_bytes, gstr,
-                       qwen3_meta, qwen3_tensors)
+from gguf_util import (ARRAY, F32, I32, STRING, U8, U32, U64, gguf_bytes, gstr, qwen3_meta,
+                       qwen3_tensors)
 
-Q4, Q6, Q8, F16 = O.Q4_K, O.Q6_K, O.Q8_0, 0
+Q4, Q5, Q6, Q8, F16 = O.Q4_K, O.Q5_K, O.Q6_K, O.Q8_0, 0
+T_Q3_K = 11
 
 
 def cfg_small():
@@ -25,7 +26,7 @@ def cfg_small():
 
 PLAN = {"embed": Q6, "lm_head": None,
         "layers": [{"q": Q4, "k": Q4, "v": Q6, "o": Q4, "gate": Q4, "up": Q4, "down": Q6},
-                   {"q": Q8, "k": Q8, "v": Q8, "o": F16, "gate": Q4, "up": Q8, "down": Q6}]}
+                   {"q": Q8, "k": Q8, "v": Q5, "o": F16, "gate": Q5, "up": Q5, "down": Q5}]}
 
 
 def inspect(path):
@@ -179,9 +180,9 @@ def test_tensor_errors(tmp_path):
     t = next(t for t in tensors if t[0] == "blk.0.attn_k.weight")
     _err(write(tmp_path, meta, with_tensor(t[0], (t[0], t[1], (t[2][0] * 2, t[2][1] // 2), t[3]))),
          "blk.0.attn_k.weight has shape")
-    # a Q5_K matrix is a supported file type but not a format this build runs
-    q5 = (t[0], T_Q5_K, t[2], b"\0" * (t[2][0] * t[2][1] // 256 * 176))
-    _err(write(tmp_path, meta, with_tensor(t[0], q5)), "unsupported ggml type Q5_K")
+    # a Q3_K matrix is a GGUF type but not a format this build runs
+    q3 = (t[0], T_Q3_K, t[2], b"\0" * (t[2][0] * t[2][1] // 256 * 110))
+    _err(write(tmp_path, meta, with_tensor(t[0], q3)), "unsupported ggml type Q3_K")
     # a low-bit norm vector is refused
     n = next(t for t in tensors if t[0] == "blk.0.attn_norm.weight")
     _err(write(tmp_path, meta, with_tensor(n[0], (n[0], 8, (256,), b"\0" * 272))),

@@ -18,7 +18,7 @@ from test_gpu_model import check_logits, check_token
 
 pytestmark = pytest.mark.gpu
 
-F16, Q8, Q4, Q6 = qutil.F16, O.Q8_0, O.Q4_K, O.Q6_K
+F16, Q8, Q4, Q5, Q6 = qutil.F16, O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K
 
 
 def configs():
@@ -38,11 +38,13 @@ def configs():
 Q4KM = {"q": Q4, "k": Q4, "v": Q6, "o": Q4, "gate": Q4, "up": Q4, "down": Q6}
 MIXED = {"q": Q8, "k": Q8, "v": Q8, "o": Q6, "gate": Q4, "up": Q8, "down": F16}
 SPLIT = {"q": Q6, "k": F16, "v": Q4, "o": F16, "gate": Q6, "up": Q6, "down": Q4}
+Q5KM = {"q": Q5, "k": Q5, "v": Q6, "o": Q5, "gate": Q5, "up": Q5, "down": Q6}
 
 PLANS = {
     "q4km-tied": {"embed": Q4, "lm_head": None, "layers": [Q4KM, MIXED]},
     "mixed-untied": {"embed": Q8, "lm_head": Q6, "layers": [SPLIT, Q4KM]},
     "f16-embed": {"embed": F16, "lm_head": Q8, "layers": [MIXED, SPLIT]},
+    "q5km-tied": {"embed": Q5, "lm_head": None, "layers": [Q5KM, MIXED]},
 }
 
 
@@ -61,7 +63,8 @@ def build(name, plan_name, seed, max_ctx):
 @pytest.mark.parametrize("name,plan,n_prompt,n_decode,max_ctx", [
     ("g2", "q4km-tied", 37, 5, 64), ("g2", "mixed-untied", 1, 3, 16),
     ("g2", "f16-embed", 20, 3, 64), ("k1024", "q4km-tied", 70, 4, 256),
-    ("k1024", "mixed-untied", 33, 3, 256), ("4b-dims-2l", "q4km-tied", 41, 3, 1024)])
+    ("k1024", "mixed-untied", 33, 3, 256), ("4b-dims-2l", "q4km-tied", 41, 3, 1024),
+    ("g2", "q5km-tied", 29, 4, 64), ("k1024", "q5km-tied", 45, 3, 256)])
 def test_qengine_prefill_and_decode_vs_oracle(gpu, name, plan, n_prompt, n_decode, max_ctx):
     print(f"qengine {name} {plan} prompt={n_prompt} decode={n_decode}", flush=True)
     cfg, eng, orc = build(name, plan, 5 + n_prompt, max_ctx)
@@ -132,7 +135,7 @@ def test_qengine_argument_errors(gpu):
             call("grout_engine_create_q", C.byref(c), C.byref(w), 0, C.byref(h))
 
     create(lambda w, L: setattr(L[0], "num_qkv_parts", 0), "num_qkv_parts")
-    create(lambda w, L: setattr(L[1].down_proj, "fmt", 13), "format 13")
+    create(lambda w, L: setattr(L[1].down_proj, "fmt", 11), "format 11")
     create(lambda w, L: setattr(L[0].o_proj, "rows", 128), "o_proj")
     create(lambda w, L: setattr(L[0].qkv[0], "rows", L[0].qkv[0].rows - 1), "qkv parts cover")
     create(lambda w, L: setattr(w.lm_head, "rows", 299), "vocab_size")
@@ -147,7 +150,7 @@ def test_qengine_argument_errors(gpu):
         QuantWeights(odd, **spec2)
 
 
-@pytest.mark.parametrize("plan", ["q4km-tied", "mixed-untied", "f16-embed"])
+@pytest.mark.parametrize("plan", ["q4km-tied", "mixed-untied", "f16-embed", "q5km-tied"])
 def test_gguf_load_vs_quantized_engine_and_oracle(gpu, tmp_path, plan):
     """A GGUF file of the same weights (norms as F32, matrices as their ggml
     blocks) loaded by grout_engine_load gives the engine built from the

@@ -1,4 +1,4 @@
-"""GPU parity of the low-bit GEMVs (Q8_0, Q4_K, Q6_K) against the ggml
+"""GPU parity of the low-bit GEMVs (Q8_0, Q4_K, Q5_K, Q6_K) against the ggml
 dequantization oracle, through the C ABI.
 
 Inputs: random ggml blocks (random payload bytes, scales/mins, d and dmin
@@ -7,8 +7,8 @@ drawn as f16 in [1e-3, 2e-2]).  The oracle runs in its decode-layout mode
 repack holds them).  Bars: the repacked weights dequantize bit-exactly (the
 kernel's fp32 dequantization rounded once to f16 equals the oracle's); GEMV
 outputs within one f16 ulp plus 1e-5 x sum(|w x| + m |x|) of the fp64 oracle
-(fp32 accumulation in another order; for Q4_K the scale and min are factored
-out of each 16-weight run, so the min term enters the bound); the SiLU-pair
+(fp32 accumulation in another order; for Q4_K and Q5_K the scale and min are
+factored out of each 16-weight run, so the min term enters the bound); the SiLU-pair
 epilogue within the bound propagated through silu(g) * u plus one ulp."""
 import ctypes as C
 
@@ -43,7 +43,7 @@ def random_blocks(fmt, n, k, seed, dmax=2e-2):
     d = rng.uniform(dmax / 20, dmax, nb).astype(np.float16).view(np.uint8).reshape(nb, 2)
     if fmt == O.Q8_0:
         b[:, 0:2] = d
-    elif fmt == O.Q4_K:
+    elif fmt in (O.Q4_K, O.Q5_K):
         b[:, 0:2] = d
         b[:, 2:4] = rng.uniform(dmax / 20, dmax, nb).astype(np.float16).view(np.uint8).reshape(nb, 2)
     else:
@@ -52,10 +52,10 @@ def random_blocks(fmt, n, k, seed, dmax=2e-2):
 
 
 def min_term(fmt, blocks, n, k):
-    """Per weight |dmin * m| (Q4_K: dequant with every q = 0), else zeros."""
-    if fmt != O.Q4_K:
+    """Per weight |dmin * m| (Q4_K, Q5_K: dequant with every q = 0), else zeros."""
+    if fmt not in (O.Q4_K, O.Q5_K):
         return np.zeros((n, k))
-    z = blocks.reshape(-1, 144).copy()
+    z = blocks.reshape(-1, O.qblock(fmt)[1]).copy()
     z[:, 16:] = 0
     return np.abs(O.dequant(fmt, z, n * k).reshape(n, k).astype(np.float64))
 
@@ -69,7 +69,7 @@ def upload(fmt, blocks, n, k, L):
     return wq
 
 
-FMTS = [(O.Q8_0, "Q8_0"), (O.Q4_K, "Q4_K"), (O.Q6_K, "Q6_K")]
+FMTS = [(O.Q8_0, "Q8_0"), (O.Q4_K, "Q4_K"), (O.Q5_K, "Q5_K"), (O.Q6_K, "Q6_K")]
 
 
 @pytest.mark.parametrize("fmt,name", FMTS)
@@ -146,6 +146,25 @@ def test_qweight_dequant_bit_exact(gpu, fmt, name):
         print(f"[dequant {name}] {len(bad)} mismatches, first at {r},{c}: got {got[r, c]} "
               f"want {want[r, c]}; cols {np.unique(bad[:, 1] % 256)[:20]}", flush=True)
     assert len(bad) == 0
+
+
+@pytest.mark.parametrize("fmt,name", FMTS)
+def test_qweight_gather_bit_exact(gpu, fmt, name):
+    """Embedding rows gathered from the repacked table equal the oracle's CPU
+    rule (fp32 scales, one rounding to f16) bit for bit; ids past the end
+    read the last row."""
+    L = gpu.lib()
+    n, k = 40, 768
+    blocks = random_blocks(fmt, n, k, seed=11 + fmt)
+    wq = upload(fmt, blocks, n, k, L)
+    ids = np.array([3, 0, 39, 17, 3, 1000], np.uint32)
+    idd = torch.from_numpy(ids.view(np.int32)).cuda()
+    out = torch.empty((len(ids), k), dtype=torch.float16, device="cuda")
+    call(L, "grout_qweight_gather", fmt, ptr(wq), n, k, ptr(idd), len(ids), ptr(out), None)
+    torch.cuda.synchronize()
+    table = O.dequant(fmt, blocks, n * k).reshape(n, k).astype(np.float16)
+    want = table[np.minimum(ids, n - 1)]
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), want.view(np.uint16))
 
 
 def test_quant_argument_errors(gpu):

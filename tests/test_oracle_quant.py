@@ -50,6 +50,22 @@ def enc_q4_k(d, dmin, sc, m, q):
     return b
 
 
+def enc_q5_k(d, dmin, sc, m, q):
+    """q: 256 values in [0, 31] in weight order; bit 4 of weight 64g + l
+    (+32) goes to bit 2g (2g+1) of qh[l]."""
+    b = np.zeros(176, np.uint8)
+    b[0:4] = np.array([f16b(d), f16b(dmin)], np.uint16).view(np.uint8)
+    b[4:16] = pack_scale_min_k4(sc, m)
+    q = np.asarray(q)
+    qh = np.zeros(32, np.uint8)
+    for g in range(4):
+        lo, hi = q[64 * g:64 * g + 32], q[64 * g + 32:64 * g + 64]
+        b[48 + 32 * g:48 + 32 * g + 32] = ((lo & 15) | ((hi & 15) << 4)).astype(np.uint8)
+        qh |= ((lo >> 4) << (2 * g)).astype(np.uint8) | ((hi >> 4) << (2 * g + 1)).astype(np.uint8)
+    b[16:48] = qh
+    return b
+
+
 def enc_q6_k(d, sc, q):
     """q: 256 6-bit values in [0, 63] in weight order (weight = d*sc*(q-32))."""
     b = np.zeros(210, np.uint8)
@@ -69,6 +85,7 @@ def enc_q6_k(d, sc, q):
 def test_block_geometry():
     assert O.qblock(O.Q8_0) == (32, 34)
     assert O.qblock(O.Q4_K) == (256, 144)
+    assert O.qblock(O.Q5_K) == (256, 176)
     assert O.qblock(O.Q6_K) == (256, 210)
 
 
@@ -120,6 +137,22 @@ def test_q4_k_decode_layout_against_encoder(seed):
     assert np.array_equal(O.dequant(O.Q6_K, b6, 256, decode=True), O.dequant(O.Q6_K, b6, 256))
 
 
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_q5_k_against_encoder(seed):
+    rng = np.random.default_rng(30 + seed)
+    d, dmin = F16(rng.uniform(1e-3, 0.1)), F16(rng.uniform(1e-3, 0.1))
+    sc, m = rng.integers(0, 64, 8), rng.integers(0, 64, 8)
+    sc[6], m[5] = 63, 63
+    q = rng.integers(0, 32, 256)
+    q[:4] = [0, 31, 16, 15]
+    blk = enc_q5_k(d, dmin, sc, m, q)
+    f32 = np.float32
+    want = (f32(d) * np.repeat(sc, 32).astype(f32)) * q.astype(f32) - \
+        f32(dmin) * np.repeat(m, 32).astype(f32)
+    for decode in (False, True):  # both modes: the reference keeps Q5_K scales as stored
+        assert np.array_equal(O.dequant(O.Q5_K, blk, 256, decode=decode), want.astype(f32))
+
+
 @pytest.mark.parametrize("seed", [0, 1])
 def test_q6_k_against_encoder(seed):
     rng = np.random.default_rng(10 + seed)
@@ -154,7 +187,8 @@ def test_bad_sizes_are_rejected():
         O.dequant(3, np.zeros(144, np.uint8), 256)
 
 
-@pytest.mark.parametrize("fmt,bound", [(O.Q8_0, 0.01), (O.Q4_K, 0.1), (O.Q6_K, 0.03)])
+@pytest.mark.parametrize("fmt,bound", [(O.Q8_0, 0.01), (O.Q4_K, 0.1), (O.Q5_K, 0.05),
+                                       (O.Q6_K, 0.03)])
 def test_test_quantizer_round_trip(fmt, bound):
     """tests/qutil.py's quantizer (used to build engine test weights) decodes,
     through the oracle, to within its quantization noise of the input."""
