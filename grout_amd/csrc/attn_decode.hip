@@ -91,7 +91,11 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES <= 4 ? 2 : 1)) void attn_decode_
   // FUSED: rotated q rows of the group, then the new K and V rows.
   __shared__ __attribute__((aligned(16))) half_t s_qkv[FUSED ? 18 : 1][kHeadDim];
 
-  const int split = blockIdx.x, kvh = blockIdx.y;
+  // block id = split * Hkv + kvh: workgroups are dealt to the 8 XCDs round
+  // robin, so with Hkv = 8 every split of a kv head runs on one XCD and its
+  // partials stay in that XCD's L2 for the merge (which uses the same map)
+  const int Hkv = (int)gridDim.x / nsplit;
+  const int kvh = (int)blockIdx.x % Hkv, split = (int)blockIdx.x / Hkv;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15, kb = lane >> 4;
@@ -147,7 +151,7 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES <= 4 ? 2 : 1)) void attn_decode_
       *reinterpret_cast<u32x2*>(&s_qkv[r][4 * j]) = yr;
       if (is_k) {
         const u32x2 vr = *reinterpret_cast<const u32x2*>(
-            fz.qkv + (size_t)(fz.Hq + (int)gridDim.y + kvh) * kHeadDim + 4 * j);
+            fz.qkv + (size_t)(fz.Hq + Hkv + kvh) * kHeadDim + 4 * j);
         *reinterpret_cast<u32x2*>(&s_qkv[G + 1][4 * j]) = vr;
         const size_t coff = (size_t)kvh * head_stride + (size_t)pos * kHeadDim + 4 * j;
         *reinterpret_cast<u32x2*>(fz.k_cache + coff) = yr;
@@ -323,7 +327,8 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES <= 4 ? 2 : 1)) void attn_decode_
   }
 }
 
-// Merge: one 128-thread workgroup per (query head h = kvh*G + g, half of D).
+// Merge: one 128-thread workgroup per (query head h = kvh*G + g, half of D),
+// block id = (2g + half) * Hkv + kvh (the split pass's XCD map).
 // Thread t owns 4 consecutive d (one float4) and every 8th split, keeps its
 // own running (max, sum, acc) so all its loads are independent, then the 8
 // split groups combine through LDS.
@@ -335,8 +340,9 @@ __global__ __launch_bounds__(128) void attn_decode_merge_kernel(
   __shared__ float s_m[kMergeGroups][16];
   __shared__ float s_l[kMergeGroups][16];
   __shared__ floatx4 s_o[kMergeGroups][16];
-  const int h = blockIdx.x, half = blockIdx.y;
-  const int kvh = h / G, g = h - kvh * G;
+  const int Hkv = (int)gridDim.x / (2 * G);
+  const int kvh = (int)blockIdx.x % Hkv, rest = (int)blockIdx.x / Hkv;
+  const int half = rest & 1, g = rest >> 1, h = kvh * G + g;
   const int dq = threadIdx.x & 15, sg = threadIdx.x >> 4;
   const int d0 = half * 64 + dq * 4;
   const size_t row0 = (size_t)kvh * nsplit * G + g;  // row of split s: row0 + s*G
@@ -382,7 +388,7 @@ hipError_t launch_attn_decode_split(const void* q, const void* k_cache, const vo
                                     int Hq, int Hkv, int nsplit, float qk_scale,
                                     float* part_acc, float* part_ml, hipStream_t stream) {
   const float scale_log2 = qk_scale * 1.4426950408889634f;
-  dim3 grid((unsigned)nsplit, (unsigned)Hkv);
+  const unsigned grid = (unsigned)(nsplit * Hkv);
   attn_decode_split_kernel<kDecWaves, false, false><<<grid, kDecWaves * 64, 0, stream>>>(
       (const half_t*)q, (const half_t*)k_cache, (const half_t*)v_cache, head_stride, d_pos,
       max_ctx, Hq / Hkv, nsplit, scale_log2, part_acc, part_ml, DecodeFused{}, nullptr);
@@ -401,13 +407,13 @@ hipError_t launch_attn_decode_fused(const void* qkv, const void* gamma_q, const 
   if (Hq / Hkv > 16) return hipErrorInvalidValue;
   if (nsplit == 1) {
     attn_decode_split_kernel<kDirectWaves, true, true>
-        <<<dim3(1u, (unsigned)Hkv), kDirectWaves * 64, 0, stream>>>(
+        <<<(unsigned)Hkv, kDirectWaves * 64, 0, stream>>>(
             nullptr, (const half_t*)k_cache, (const half_t*)v_cache, head_stride, d_pos, max_ctx,
             Hq / Hkv, 1, scale_log2, nullptr, nullptr, fz, (half_t*)out);
     return hipGetLastError();
   }
   attn_decode_split_kernel<kDecWaves, true, false>
-      <<<dim3((unsigned)nsplit, (unsigned)Hkv), kDecWaves * 64, 0, stream>>>(
+      <<<(unsigned)(nsplit * Hkv), kDecWaves * 64, 0, stream>>>(
           nullptr, (const half_t*)k_cache, (const half_t*)v_cache, head_stride, d_pos, max_ctx,
           Hq / Hkv, nsplit, scale_log2, part_acc, part_ml, fz, nullptr);
   const hipError_t e = hipGetLastError();
@@ -417,7 +423,7 @@ hipError_t launch_attn_decode_fused(const void* qkv, const void* gamma_q, const 
 
 hipError_t launch_attn_decode_merge(const float* part_acc, const float* part_ml, void* out,
                                     int Hq, int Hkv, int nsplit, hipStream_t stream) {
-  attn_decode_merge_kernel<<<dim3((unsigned)Hq, 2), 128, 0, stream>>>(part_acc, part_ml,
+  attn_decode_merge_kernel<<<(unsigned)(2 * Hq), 128, 0, stream>>>(part_acc, part_ml,
                                                                       (half_t*)out, Hq / Hkv, nsplit);
   return hipGetLastError();
 }
