@@ -481,11 +481,14 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
   };
 
   // ---- prologue: K(0) -> k0, V(0) -> v0, K(1) -> k1, Q of the first block ----
+  // Team B loads its Q only after the first barrier (it idles one phase
+  // anyway), so team A's Q is not slowed by the other half of the burst of Q
+  // reads that opens the kernel on every CU at once.
   if (n > 0) {
     dma_tile(is_k, kh, tile_at(0), k0);
     dma_tile(is_v, vh, tile_at(0), v0);
     dma_tile(is_k, kh, tile_at(min(1, n - 1)), k1);
-    load_q(qb0);
+    if (team == 0) load_q(qb0);
   }
   wait_vm_all();
   lds_barrier();
@@ -494,6 +497,7 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
   const int total = max(1 + 2 * a, 2 + 2 * nB);
   int mine = 0;
   if (team == 1) {
+    if (n > 0) load_q(qb0);  // waited for before its first S.K^T (vmcnt)
     lds_barrier();
     mine = 1;
   }
