@@ -370,15 +370,14 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
   // then mask, row max, lazy rescale, P(j) and its row sums.  Ends with each
   // wave's loads of the previous S phase complete.
   auto s_phase = [&](int j, unsigned char* kfill, unsigned char* vfill) __attribute__((always_inline)) {
+    // Once per workgroup (team B, before the first tile of its second
+    // block): that block's Q, issued ahead of this phase's 8 tile loads.  The
+    // phase's closing vmcnt(8) then covers it, so its latency hides under the
+    // softmax, and the wait the compiler puts before the next S.K^T is the
+    // same vmcnt(8) (8 tile loads issued after it), already satisfied.
+    if (j + 1 == n0 && n1 > 0) load_q(qb1);
     dma_tile(is_k, kh, tile_at(min(j + 2, n - 1)), kfill);
     dma_tile(is_v, vh, tile_at(min(j + 1, n - 1)), vfill);
-    if (j + 1 == n0 && n1 > 0) {
-      // Once per workgroup: the next segment's Q, waited for here, so that
-      // no load into qf is pending where the paths join (the waitcnt pass
-      // would otherwise wait for every load in flight before each S.K^T).
-      load_q(qb1);
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    }
     const int kv0 = tile_at(j) * kBN;
     const int qrow0 = pos0 + qb_at(j) * BQ;  // first query position of the block
     if (kv0 + kBN - 1 > qrow0) {
