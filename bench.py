@@ -36,8 +36,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--only", default="",
-                    help="comma list: decode32b,prefill,decode4b,norm,engine4b,engine4b_q4km (gemv, qgemv: only "
-                         "when named)")
+                    help="comma list: decode32b,prefill,decode4b,norm,engine4b,engine4b_q4km (gemv, qgemv, "
+                         "engine4b_q5km: only when named)")
     ap.add_argument("--eager", action="store_true",
                     help="launch the timed calls from the host instead of replaying a captured "
                          "graph (for per-dispatch counter collection)")
@@ -257,10 +257,11 @@ def bench_engine(prompt_len=512, decode_steps=256, max_ctx=1024):
                 distinct_tokens=len(set(toks)), mean_ctx=mean_ctx)
 
 
-def q4km_formats(n_layers):
+def q4km_formats(n_layers, base=12):
     """Q4_K_M-style mix: attn_v and ffn_down in Q6_K for the first and last
-    eighth of the layers and every third layer between, Q4_K elsewhere."""
-    Q4, Q6 = 12, 14
+    eighth of the layers and every third layer between, Q4_K elsewhere (base=13:
+    the Q5_K_M mix, Q5_K in place of Q4_K)."""
+    Q4, Q6 = base, 14
 
     def more_bits(l):
         return l < n_layers // 8 or l >= 7 * n_layers // 8 or (l - n_layers // 8) % 3 == 2
@@ -271,16 +272,17 @@ def q4km_formats(n_layers):
     return fmts
 
 
-def bench_engine_q(prompt_len=512, decode_steps=256, max_ctx=1024):
+def bench_engine_q(prompt_len=512, decode_steps=256, max_ctx=1024, base=12):
     """Config 5 over low-bit weights: the Qwen3-4B engine with random
     GGUF-block weights in a Q4_K_M-style mix (q4km_formats; Q6_K tied
-    embedding / lm_head), prompt and timing as bench_engine."""
+    embedding / lm_head; base=13 for the Q5_K_M mix), prompt and timing as
+    bench_engine."""
     import numpy as np
     import torch
     from grout_amd.model import Engine, QuantWeights, Qwen3Config
 
     cfg = Qwen3Config.qwen3_4b()
-    qw = QuantWeights.random(cfg, q4km_formats(cfg.num_layers), embed_fmt=14, seed=0)
+    qw = QuantWeights.random(cfg, q4km_formats(cfg.num_layers, base), embed_fmt=14, seed=0)
     torch.cuda.synchronize()
     eng = Engine.from_quantized(cfg, qw, max_ctx=max_ctx)
     prompt = np.random.default_rng(512).integers(0, cfg.vocab_size, prompt_len)
@@ -496,6 +498,9 @@ def main():
     if want("engine4b_q4km"):
         res["engine4b_q4km"] = bench_engine_q()
         print(f"# engine4b_q4km {res['engine4b_q4km']}", file=sys.stderr, flush=True)
+    if "engine4b_q5km" in only:
+        res["engine4b_q5km"] = bench_engine_q(base=13)
+        print(f"# engine4b_q5km {res['engine4b_q5km']}", file=sys.stderr, flush=True)
 
     line = {"metric": "decode-attn HBM GB/s (% of peak) + prefill FMHA TFLOP/s (% MFMA peak)",
             "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "higher_is_better": True,
@@ -556,6 +561,17 @@ def main():
         line["engine4b_q4km"] = {
             "workload": "qwen3-4b engine, random GGUF-block weights in a Q4_K_M-style mix "
                         "(Q4_K; attn_v / ffn_down Q6_K in 18 of 36 layers; Q6_K tied embedding), "
+                        "512-token prompt, 256 greedy decode steps (decode-step hipGraph)",
+            "decode_tok_s": round(r["tok_s"], 1), "decode_ms_per_token": round(r["decode_ms"], 4),
+            "prefill_512_ms": round(r["prefill_ms"], 2),
+            "weight_bytes": r["weight_bytes"],
+            "weight_stream_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    if "engine4b_q5km" in res:
+        r = res["engine4b_q5km"]
+        gbs = r["bytes_per_token"] * r["tok_s"] / 1e9
+        line["engine4b_q5km"] = {
+            "workload": "qwen3-4b engine, random GGUF-block weights in a Q5_K_M-style mix "
+                        "(Q5_K; attn_v / ffn_down Q6_K in 18 of 36 layers; Q6_K tied embedding), "
                         "512-token prompt, 256 greedy decode steps (decode-step hipGraph)",
             "decode_tok_s": round(r["tok_s"], 1), "decode_ms_per_token": round(r["decode_ms"], 4),
             "prefill_512_ms": round(r["prefill_ms"], 2),
