@@ -198,7 +198,7 @@ def test_decode_reuses_workspace_across_calls(gpu):
 
 @pytest.mark.parametrize("S,Hq,Hkv,pos0", [
     (1, 32, 8, 0), (17, 32, 8, 0), (64, 16, 8, 3), (200, 32, 8, 77), (130, 64, 8, 0),
-    (96, 8, 8, 10), (77, 40, 8, 9), (33, 16, 1, 0)])
+    (96, 8, 8, 10), (77, 40, 8, 9), (33, 16, 1, 0), (150, 48, 8, 5), (111, 56, 8, 0)])
 def test_prefill_attention_vs_oracle(gpu, S, Hq, Hkv, pos0):
     _say("prefill", S, Hq, Hkv, pos0)
     max_ctx = pos0 + S + 5
@@ -213,13 +213,13 @@ def test_prefill_attention_vs_oracle(gpu, S, Hq, Hkv, pos0):
 @pytest.mark.parametrize("paired", [0, 1])
 @pytest.mark.parametrize("S,Hq,Hkv,pos0", [
     (1, 32, 8, 0), (17, 32, 8, 0), (130, 64, 8, 0), (200, 32, 8, 77), (77, 40, 8, 9),
-    (33, 16, 1, 0), (700, 32, 8, 100), (1000, 16, 4, 0), (2048, 24, 8, 0)])
+    (33, 16, 1, 0), (700, 32, 8, 100), (1000, 16, 4, 0), (2048, 24, 8, 0), (600, 56, 8, 7)])
 def test_prefill_work_splits_vs_oracle(gpu, monkeypatch, paired, S, Hq, Hkv, pos0):
     """Both work splits of the prefill kernel (a q block per workgroup, its
     tiles split over the two 4-wave teams; complementary q-block pairs, team B
     taking the light block and the tail of the heavy one), forced through
     GROUT_FMHA_PREFILL_PAIRED, on odd block counts, a kv prefix (pos0 > 0), a
-    single kv head and HG = 3 (rows that fall outside a 126-row block)."""
+    single kv head, HG = 3 (rows that fall outside a 126-row block) and HG = 7."""
     monkeypatch.setenv("GROUT_FMHA_PREFILL_PAIRED", str(paired))
     _say("prefill_split", paired, S, Hq, Hkv, pos0)
     max_ctx = pos0 + S + 3
