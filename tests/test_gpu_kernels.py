@@ -113,6 +113,9 @@ def _decode_case(gpu, Hq, Hkv, ctx, max_ctx, num_splits, tag):
     (8, 8, 1, 64, None),          # ctx = 1, G = 1
     (32, 2, 100, 160, 3),         # ragged ctx, G = 16
     (40, 8, 777, 1000, None),     # G = 5
+    (16, 1, 1500, 2048, None),    # one kv head (G = 16)
+    (28, 4, 900, 1024, 5),        # Hkv = 4, G = 7
+    (32, 16, 2000, 2048, None),   # Hkv = 16, G = 2
 ])
 def test_decode_attention_vs_oracle(gpu, Hq, Hkv, ctx, max_ctx, splits):
     _decode_case(gpu, Hq, Hkv, ctx, max_ctx, splits, f"dec{Hq}_{ctx}")
@@ -127,6 +130,8 @@ def test_decode_attention_vs_oracle(gpu, Hq, Hkv, ctx, max_ctx, splits):
     (40, 8, 16, 64, 1),           # G = 5, the new row opens a tile
     (8, 8, 0, 64, 1),             # first position
     (16, 8, 47, 64, 7),           # more splits than tiles
+    (16, 1, 300, 512, None),      # one kv head
+    (28, 4, 200, 256, 3),         # Hkv = 4, G = 7
 ])
 def test_fused_decode_step_vs_oracle(gpu, Hq, Hkv, pos, max_ctx, splits):
     """Norm/RoPE/KV write fused into the decode attention: cache rows
