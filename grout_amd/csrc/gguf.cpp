@@ -51,6 +51,8 @@ enum : uint32_t {
 
 // ggml tensor types this loader reads.
 enum : uint32_t { kTF32 = 0, kTF16 = 1, kTQ8_0 = 8, kTQ4_K = 12, kTQ5_K = 13, kTQ6_K = 14, kTBF16 = 30 };
+// ggml types a GGUF file may hold that this loader refuses (named in errors)
+enum : uint32_t { kTQ4_0 = 2, kTQ4_1 = 3, kTQ5_0 = 6, kTQ5_1 = 7, kTQ8_1 = 9, kTQ2_K = 10, kTQ3_K = 11, kTQ8_K = 15 };
 
 // (weights per block, bytes per block), or (0, 0) for types not read here.
 void type_block(uint32_t t, uint64_t* be, uint64_t* bb) {
@@ -76,15 +78,14 @@ const char* type_name(uint32_t t) {
     case kTQ4_K: return "Q4_K";
     case kTQ5_K: return "Q5_K";
     case kTQ6_K: return "Q6_K";
-    // types a GGUF file may hold that this loader does not read
-    case 2: return "Q4_0";
-    case 3: return "Q4_1";
-    case 6: return "Q5_0";
-    case 7: return "Q5_1";
-    case 9: return "Q8_1";
-    case 10: return "Q2_K";
-    case 11: return "Q3_K";
-    case 15: return "Q8_K";
+    case kTQ4_0: return "Q4_0";
+    case kTQ4_1: return "Q4_1";
+    case kTQ5_0: return "Q5_0";
+    case kTQ5_1: return "Q5_1";
+    case kTQ8_1: return "Q8_1";
+    case kTQ2_K: return "Q2_K";
+    case kTQ3_K: return "Q3_K";
+    case kTQ8_K: return "Q8_K";
     default: return "?";
   }
 }

@@ -676,6 +676,7 @@ __device__ __forceinline__ QRaw qload(const uint8_t* __restrict__ W, const QLayo
     r.a = load_stream16(W + L.off[0] + (size_t)row * K + (size_t)j * 16);
   } else if (FMT == 12) {
     r.a = load_stream16(W + L.off[0] + (size_t)row * (K / 2) + (size_t)j * 16);
+    r.b = u32x4{0u, 0u, 0u, 0u};  // no fifth bits
   } else if (FMT == 13) {
     r.a = load_stream16(W + L.off[0] + (size_t)row * (K / 2) + (size_t)j * 16);
     r.b = load_stream16(W + L.off[2] + (size_t)row * (K / 8) + (size_t)(j >> 3) * 32 + (j & 1) * 16);
