@@ -21,10 +21,10 @@ import sys
 import time
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
-# HBM bytes per split-kernel launch (Qwen3-32B, ctx 32768, 32 splits) measured with
-# rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by a plain-copy calibration (x2.0, x1.0);
-# see profiles/attn_decode_split_qwen3-32b_ctx32768.md.
-DECODE32B_TRAFFIC_BYTES = 134.31e6 + 1.065e6
+# HBM bytes per split-kernel launch (Qwen3-32B, ctx 32768) by split count, measured with
+# rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by a plain-copy calibration (x2.0, x1.0).
+DECODE32B_TRAFFIC_BYTES = {32: 134.31e6 + 1.065e6}
+DECODE32B_TRAFFIC_SOURCE = "profiles/attn_decode_split_qwen3-32b_ctx32768.md"
 F16_MFMA_PEAK_TFLOPS = 2516.6  # MI355X dense fp16 MFMA, TFLOP/s
 D = 128
 
@@ -87,49 +87,107 @@ def time_launches(fn, steps, warmup, stream=None, graph=None):
     return ms
 
 
+class DecodeBench:
+    """Decode attention over n_layers rotating layer caches [Hkv][max_ctx][128]
+    (more bytes than the 256 MB Infinity Cache, so K/V stream from HBM); one
+    step = one layer's split pass + merge (grout_attn_decode)."""
+
+    def __init__(self, Hq, Hkv, max_ctx, n_layers):
+        import torch
+
+        dev = torch.device("cuda")
+        g = torch.Generator(device=dev).manual_seed(1234)
+        self.Hq, self.Hkv, self.max_ctx, self.n = Hq, Hkv, max_ctx, n_layers
+        self.kcs = [torch.randn((Hkv, max_ctx, D), generator=g, device=dev, dtype=torch.float16)
+                    for _ in range(n_layers)]
+        self.vcs = [torch.randn((Hkv, max_ctx, D), generator=g, device=dev, dtype=torch.float16)
+                    for _ in range(n_layers)]
+        self.q = torch.randn((Hq, D), generator=g, device=dev, dtype=torch.float16)
+        self.out = torch.empty_like(self.q)
+        self.dev = dev
+
+    def alg_bytes(self, ctx):
+        return 2 * self.Hkv * ctx * D * 2 + 2 * self.Hq * D * 2
+
+    def time_step(self, ctx, ns, steps, warmup):
+        import torch
+        from grout_amd import ops
+
+        pos = torch.tensor([ctx - 1], dtype=torch.int32, device=self.dev)
+        ws = ops.decode_workspace(self.Hq, self.Hkv, ns, self.dev)
+
+        def step(i=0):
+            j = i % self.n
+            ops.attn_decode(self.q, self.kcs[j], self.vcs[j], pos, num_splits=ns, out=self.out,
+                            workspace=ws)
+
+        return time_launches(step, steps, warmup)
+
+    def time_split(self, ctx, ns, steps, warmup):
+        import ctypes as C
+        import torch
+        from grout_amd import ops
+        from grout_amd._lib import call
+
+        pos = torch.tensor([ctx - 1], dtype=torch.int32, device=self.dev)
+        ws = ops.decode_workspace(self.Hq, self.Hkv, ns, self.dev)
+        G = self.Hq // self.Hkv
+        acc = ws[: self.Hkv * ns * G * D]
+        ml = ws[self.Hkv * ns * G * D:]
+        qp, pp = C.c_void_p(self.q.data_ptr()), C.c_void_p(pos.data_ptr())
+        kps = [C.c_void_p(t.data_ptr()) for t in self.kcs]
+        vps = [C.c_void_p(t.data_ptr()) for t in self.vcs]
+        ap, mp = C.c_void_p(acc.data_ptr()), C.c_void_p(ml.data_ptr())
+
+        def split_only(i=0):
+            j = i % self.n
+            sp = C.c_void_p(torch.cuda.current_stream().cuda_stream)  # the capture stream
+            call("grout_fmha_decode_gqa_split", qp, kps[j], vps[j], ap, mp, pp, self.Hq,
+                 self.Hkv, D, self.max_ctx, self.max_ctx * D, ns, 1.0 / math.sqrt(D), sp)
+
+        return time_launches(split_only, steps, warmup)
+
+    def close(self):
+        import torch
+
+        del self.kcs, self.vcs
+        torch.cuda.empty_cache()
+
+
 def bench_decode(ops, Hq, Hkv, ctx, max_ctx, n_layers, steps, warmup, num_splits=None):
-    import torch
-
-    dev = torch.device("cuda")
-    stream = torch.cuda.current_stream(dev)
-    g = torch.Generator(device=dev).manual_seed(1234)
-    kcs = [torch.randn((Hkv, max_ctx, D), generator=g, device=dev, dtype=torch.float16)
-           for _ in range(n_layers)]
-    vcs = [torch.randn((Hkv, max_ctx, D), generator=g, device=dev, dtype=torch.float16)
-           for _ in range(n_layers)]
-    q = torch.randn((Hq, D), generator=g, device=dev, dtype=torch.float16)
-    out = torch.empty_like(q)
-    pos = torch.tensor([ctx - 1], dtype=torch.int32, device=dev)
+    b = DecodeBench(Hq, Hkv, max_ctx, n_layers)
     ns = num_splits or ops.default_splits(max_ctx, Hq, Hkv)
-    ws = ops.decode_workspace(Hq, Hkv, ns, dev)
-    G = Hq // Hkv
-    acc = ws[: Hkv * ns * G * D].view(Hkv, ns, G, D)
-    ml = ws[Hkv * ns * G * D:].view(Hkv, ns, G, 2)
+    r = dict(step_ms=b.time_step(ctx, ns, steps, warmup),
+             split_ms=b.time_split(ctx, ns, steps, warmup), alg_bytes=b.alg_bytes(ctx),
+             num_splits=ns)
+    b.close()
+    return r
 
-    def step(i=0):
-        j = i % n_layers
-        ops.attn_decode(q, kcs[j], vcs[j], pos, num_splits=ns, out=out, workspace=ws)
 
-    from grout_amd._lib import call
-    import ctypes as C
+DECODE32B_SPLITS = (8, 16, 24, 32, 40, 48, 64)
 
-    qp, pp = C.c_void_p(q.data_ptr()), C.c_void_p(pos.data_ptr())
-    kps = [C.c_void_p(t.data_ptr()) for t in kcs]
-    vps = [C.c_void_p(t.data_ptr()) for t in vcs]
-    ap, mp = C.c_void_p(acc.data_ptr()), C.c_void_p(ml.data_ptr())
 
-    def split_only(i=0):
-        j = i % n_layers
-        sp = C.c_void_p(torch.cuda.current_stream().cuda_stream)  # the capture stream
-        call("grout_fmha_decode_gqa_split", qp, kps[j], vps[j], ap, mp, pp, Hq, Hkv, D, max_ctx,
-             max_ctx * D, ns, 1.0 / math.sqrt(D), sp)
-
-    step_ms = time_launches(step, steps, warmup, stream)
-    split_ms = time_launches(split_only, steps, warmup, stream)
-    alg_bytes = 2 * Hkv * ctx * D * 2 + 2 * Hq * D * 2
-    del kcs, vcs
-    torch.cuda.empty_cache()
-    return dict(step_ms=step_ms, split_ms=split_ms, alg_bytes=alg_bytes, num_splits=ns)
+def bench_decode32b_sweep(ops, ctxs, steps, warmup, sweep_steps=100):
+    """Config 4: Qwen3-32B decode attention (Hq=64, Hkv=8) at each context.
+    The split count is swept first (sweep_steps graph-replayed steps of split
+    pass + merge per candidate), as the reference tunes FMHA_NUM_KV_SPLITS per
+    context (src/model.rs:135-141, benchmarks/sweep_tg_sm100.sh:32-43); the
+    fastest is then timed afresh over `steps` steps, so the reported time is
+    not the minimum of the sweep's samples."""
+    b = DecodeBench(64, 8, 32768, 4)
+    out = {}
+    for ctx in ctxs:
+        sweep = {ns: b.time_step(ctx, ns, sweep_steps, warmup) for ns in DECODE32B_SPLITS}
+        best = min(sweep, key=sweep.get)
+        out[ctx] = dict(step_ms=b.time_step(ctx, best, steps, warmup),
+                        split_ms=b.time_split(ctx, best, steps, warmup),
+                        alg_bytes=b.alg_bytes(ctx), num_splits=best,
+                        default_splits=ops.default_splits(32768, 64, 8),
+                        sweep_us={ns: round(ms * 1e3, 2) for ns, ms in sweep.items()})
+        print(f"# decode32b ctx={ctx} best={best} {out[ctx]['sweep_us']}", file=sys.stderr,
+              flush=True)
+    b.close()
+    return out
 
 
 def bench_decode_graph(grout_amd, Hq, Hkv, ctx, max_ctx, n_layers, steps, warmup):
@@ -415,33 +473,94 @@ def bench_qgemv(steps, warmup):
     return out
 
 
-def cpu_baseline_decode(Hq, Hkv, ctx):
-    """Scalar fp32 oracle (single thread) on one 32B decode layer: 16 of the 64
-    query heads (2 kv heads) at full context; GB/s scaled to the whole layer."""
+def host_cpu():
+    """CPU model name, logical CPU count and the CPUs this process may use."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count() or 1
+    return model, os.cpu_count() or 1, usable
+
+
+def cpu_threads(limit):
+    """All-core thread count: the CPUs this process may use, capped by
+    OMP_NUM_THREADS when set (the GPU box's CPU share) and by `limit`."""
+    _, _, usable = host_cpu()
+    n = usable
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, min(n, limit))
+
+
+def _timed(fn, min_s, max_reps=1000):
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        fn()
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_s or reps >= max_reps:
+            return dt / reps, reps
+
+
+def cpu_baseline(Hq=64, Hkv=8, ctx=32768, S=2048, pHq=32, pHkv=8):
+    """The scalar fp32 oracle (oracle/grout_oracle.c, gcc -O2, no fast-math)
+    timed on this host's cores on the same workloads as the GPU lines:
+    * decode: one full Qwen3-32B layer (Hq=64, Hkv=8) at ctx 32768, single
+      thread and all-core (threads over query heads); GB/s of the same
+      algorithmic bytes as the GPU line;
+    * prefill: Qwen3-4B causal attention at S=2048 on sampled rows (every 32nd
+      row, all 32 heads), all-core; TFLOP/s over those rows' exact
+      4*Hq*128*(row+1) FLOP."""
     import numpy as np
 
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     import oracle as O
 
-    hq_s, hkv_s = 16, 2
-    q = O.fill_normal_f16(O.seed_for("bq"), (hq_s, D))
-    kc = O.fill_normal_f16(O.seed_for("bk"), (hkv_s, ctx, D))
-    vc = O.fill_normal_f16(O.seed_for("bv"), (hkv_s, ctx, D))
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
-        O.attention_decode(q, kc, vc, ctx - 1, nthreads=1)
-        reps += 1
-        if time.perf_counter() - t0 > 10.0:
-            break
-    dt = (time.perf_counter() - t0) / reps
-    layer_s = dt * (Hq / hq_s)
-    alg_bytes = 2 * Hkv * ctx * D * 2 + 2 * Hq * D * 2
-    return dict(value=alg_bytes / layer_s / 1e9, unit="GB/s", cores=1, kind="port",
-                sample=f"oracle/grout_oracle.c go_attention_decode, 1 thread, {hq_s} q heads x "
-                       f"{hkv_s} kv heads at ctx {ctx} ({reps} reps, {dt*1e3:.1f} ms each), "
-                       f"scaled x{Hq // hq_s} to the full Hq={Hq} layer",
-                layer_ms=layer_s * 1e3)
+    model, ncpu, usable = host_cpu()
+    nthr = cpu_threads(Hq)
+    q = O.fill_normal_f16(O.seed_for("bq"), (Hq, D))
+    kc = O.fill_normal_f16(O.seed_for("bk"), (Hkv, ctx, D))
+    vc = O.fill_normal_f16(O.seed_for("bv"), (Hkv, ctx, D))
+    alg = 2 * Hkv * ctx * D * 2 + 2 * Hq * D * 2
+    t1, r1 = _timed(lambda: O.attention_decode(q, kc, vc, ctx - 1, nthreads=1), 4.0)
+    tn, rn = _timed(lambda: O.attention_decode(q, kc, vc, ctx - 1, nthreads=nthr), 4.0)
+    del kc, vc
+    pq = O.fill_normal_f16(O.seed_for("pbq"), (S, pHq, D))
+    pk = O.fill_normal_f16(O.seed_for("pbk"), (pHkv, S, D))
+    pv = O.fill_normal_f16(O.seed_for("pbv"), (pHkv, S, D))
+    rows = np.arange(31, S, 32, dtype=np.int32)
+    pflop = float(sum(4.0 * pHq * D * (int(r) + 1) for r in rows))
+    pthr = cpu_threads(pHq)
+    tp, rp = _timed(lambda: O.attention_prefill_rows(pq, pk, pv, 0, rows=rows, nthreads=pthr),
+                    3.0)
+    tp1, rp1 = _timed(lambda: O.attention_prefill_rows(pq, pk, pv, 0, rows=rows[::8],
+                                                       nthreads=1), 2.0)
+    pflop1 = float(sum(4.0 * pHq * D * (int(r) + 1) for r in rows[::8]))
+    return dict(
+        value=alg / tn / 1e9, unit="GB/s", cores=nthr, kind="port",
+        sample=f"oracle/grout_oracle.c go_attention_decode, one full Qwen3-32B decode layer "
+               f"(Hq={Hq}, Hkv={Hkv}, ctx {ctx}), {nthr} threads over query heads, "
+               f"{rn} reps of {tn * 1e3:.1f} ms",
+        cpu_model=model, cpu_count=ncpu, cpus_usable=usable,
+        layer_ms=tn * 1e3,
+        single_thread={"value": alg / t1 / 1e9, "unit": "GB/s", "cores": 1,
+                       "layer_ms": t1 * 1e3, "reps": r1},
+        prefill={"workload": f"qwen3-4b causal prefill attention S={S} Hq={pHq} Hkv={pHkv}, "
+                             f"{len(rows)} sampled rows (every 32nd), all heads",
+                 "tflops": pflop / tp / 1e12, "cores": pthr, "ms": tp * 1e3, "reps": rp,
+                 "single_thread_tflops": pflop1 / tp1 / 1e12,
+                 "single_thread_rows": int(len(rows[::8]))})
 
 
 def main():
@@ -469,11 +588,16 @@ def main():
     want = lambda k: not only or k in only
     res = {}
     if want("decode32b"):
-        res["decode32b"] = bench_decode(ops, 64, 8, 32768, 32768, 4, a.steps, a.warmup)
+        res["decode32b_sweep"] = bench_decode32b_sweep(ops, (8192, 16384, 32768), a.steps,
+                                                       a.warmup)
+        res["decode32b"] = res["decode32b_sweep"][32768]
         print(f"# decode32b {res['decode32b']}", file=sys.stderr, flush=True)
     if want("prefill"):
-        res["prefill"] = bench_prefill(ops, 2048, 32, 8, max(a.steps // 4, 10), a.warmup)
-        print(f"# prefill {res['prefill']}", file=sys.stderr, flush=True)
+        res["prefill_sweep"] = {S: bench_prefill(ops, S, 32, 8, max(a.steps // (4 if S < 8192 else 10), 10),
+                                                 a.warmup)
+                                for S in (512, 2048, 8192)}
+        res["prefill"] = res["prefill_sweep"][2048]
+        print(f"# prefill {res['prefill_sweep']}", file=sys.stderr, flush=True)
     if want("decode4b"):
         res["decode4b"] = bench_decode(ops, 32, 8, 4096, 32768, 36, a.steps, a.warmup)
         res["graph4b_ms"] = bench_decode_graph(grout_amd, 32, 8, 4096, 32768, 36,
@@ -513,13 +637,24 @@ def main():
         line["config"] = {"workload": "qwen3-32b decode attention (split-K + LSE merge), Hq=64 "
                                       "Hkv=8 D=128, ctx 32768, batch 1, 4 rotating layer caches",
                           "num_splits": r["num_splits"], "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        traffic = DECODE32B_TRAFFIC_BYTES.get(r["num_splits"])
         line["roofline"] = {"bound": "hbm", "kernel": "attn_decode_split_kernel",
                             "achieved": round(split_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": round(split_gbs / HBM_PEAK_GBS, 4),
-                            "traffic": DECODE32B_TRAFFIC_BYTES if r["num_splits"] == 32 else None,
-                            "traffic_source": "profiles/attn_decode_split_qwen3-32b_ctx32768.md",
+                            "traffic": traffic,
+                            "traffic_source": DECODE32B_TRAFFIC_SOURCE if traffic else None,
                             "kernel_us": round(r["split_ms"] * 1e3, 3),
                             "alg_bytes_per_launch": r["alg_bytes"]}
+        sweep = {}
+        for ctx, rr in res["decode32b_sweep"].items():
+            g = rr["alg_bytes"] / (rr["step_ms"] * 1e-3) / 1e9
+            sg = rr["alg_bytes"] / (rr["split_ms"] * 1e-3) / 1e9
+            sweep[str(ctx)] = {"num_splits": rr["num_splits"], "step_us": round(rr["step_ms"] * 1e3, 2),
+                               "step_gbs": round(g, 1), "step_hbm_frac": round(g / HBM_PEAK_GBS, 4),
+                               "split_us": round(rr["split_ms"] * 1e3, 2),
+                               "split_gbs": round(sg, 1), "split_hbm_frac": round(sg / HBM_PEAK_GBS, 4),
+                               "alg_bytes": rr["alg_bytes"], "splits_swept_us": rr["sweep_us"]}
+        line["decode32b_sweep"] = sweep
     if "prefill" in res:
         r = res["prefill"]
         tf = r["flop"] / (r["ms"] * 1e-3) / 1e12
@@ -527,6 +662,12 @@ def main():
                            "us": round(r["ms"] * 1e3, 2), "tflops": round(tf, 1),
                            "mfma_frac": round(tf / F16_MFMA_PEAK_TFLOPS, 4),
                            "flop": r["flop"]}
+        sweep = {}
+        for S, rr in res["prefill_sweep"].items():
+            t = rr["flop"] / (rr["ms"] * 1e-3) / 1e12
+            sweep[str(S)] = {"us": round(rr["ms"] * 1e3, 2), "tflops": round(t, 1),
+                             "mfma_frac": round(t / F16_MFMA_PEAK_TFLOPS, 4), "flop": rr["flop"]}
+        line["prefill_sweep"] = sweep
     if "decode4b" in res:
         r = res["decode4b"]
         gbs = r["alg_bytes"] / (r["step_ms"] * 1e-3) / 1e9
@@ -578,8 +719,15 @@ def main():
             "weight_bytes": r["weight_bytes"],
             "weight_stream_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
     if not a.no_cpu and "decode32b" in res:
-        cb = cpu_baseline_decode(64, 8, 32768)
-        line["cpu_baseline"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in cb.items()}
+        cb = cpu_baseline()
+
+        def rnd(v):
+            if isinstance(v, float):
+                return round(v, 4)
+            if isinstance(v, dict):
+                return {k: rnd(x) for k, x in v.items()}
+            return v
+        line["cpu_baseline"] = rnd(cb)
     print(json.dumps(line), flush=True)
     return 0
 

@@ -129,6 +129,10 @@ SIGNATURES = {
     "grout_engine_decode_greedy": (_i, [_p, _u32, _p]),
     "grout_engine_reset": (_i, [_p]),
     "grout_engine_position": (_i, [_p]),
+    "grout_engine_vram_preflight": (_i, [C.POINTER(Qwen3Config), _sz, _sz, _sz, _sz,
+                                         C.POINTER(_sz)]),
+    "grout_engine_uses_decode_graph": (_i, [_p]),
+    "grout_engine_decode_graph_error": (C.c_char_p, [_p]),
     "grout_engine_destroy": (_i, [_p]),
 }
 

@@ -67,6 +67,9 @@ inline int check_ptrs16(std::initializer_list<std::pair<const void*, const char*
 }
 
 inline int check_stride(long kv_head_stride, long min_rows) {
+  GROUT_NEED(min_rows <= GROUT_MAX_CTX, GROUT_ENOTSUP,
+             "cache length %ld exceeds GROUT_MAX_CTX=%d (32-bit row offsets)", min_rows,
+             GROUT_MAX_CTX);
   GROUT_NEED(kv_head_stride % 8 == 0, GROUT_EALIGN,
              "kv_head_stride=%ld elements is not a multiple of 8 (16 bytes)", kv_head_stride);
   GROUT_NEED(kv_head_stride >= min_rows * 128, GROUT_EINVAL,

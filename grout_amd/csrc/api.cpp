@@ -18,7 +18,7 @@ extern "C" {
 
 const char* grout_last_error(void) { return g_last_error.c_str(); }
 
-int grout_abi_version(void) { return (1 << 16) | 0; }
+int grout_abi_version(void) { return (1 << 16) | 1; }
 
 int grout_rope_inv_freq(int head_dim, float theta, float* inv_freq) {
   GROUT_NEED(head_dim > 0 && head_dim % 2 == 0, GROUT_EINVAL, "head_dim=%d must be even",
@@ -272,8 +272,8 @@ int grout_decode_graph_create(const grout_decode_layer* layers, int num_layers,
   for (int i = 0; i < num_layers; ++i) {
     const grout_decode_layer& L = layers[i];
     const int rc = check_ptrs16({{L.qkv, "qkv"}, {L.gamma_q, "gamma_q"}, {L.gamma_k, "gamma_k"},
-                                 {L.q_rope, "q_rope"}, {L.k_cache, "k_cache"},
-                                 {L.v_cache, "v_cache"}, {L.attn_out, "attn_out"}});
+                                 {L.k_cache, "k_cache"}, {L.v_cache, "v_cache"},
+                                 {L.attn_out, "attn_out"}});
     if (rc != GROUT_OK) return fail(rc, "layer %d: %s", i, g_last_error.c_str());
   }
   const size_t need = decode_ws_bytes(num_q_heads, num_kv_heads, num_splits);
@@ -283,23 +283,26 @@ int grout_decode_graph_create(const grout_decode_layer* layers, int num_layers,
   grout_decode_graph* g = new (std::nothrow) grout_decode_graph();
   GROUT_NEED(g != nullptr, GROUT_EINVAL, "out of host memory");
   g->max_ctx = max_ctx;
-  hipStream_t cap = nullptr;
+  // Capture on the caller's stream; the legacy NULL stream cannot be
+  // captured, so a NULL stream gets a private one for the capture only.
+  hipStream_t cap = as_stream(stream);
+  hipStream_t own = nullptr;
   int rc = hip_status(hipMalloc(&g->d_pos, sizeof(uint32_t)), "hipMalloc(position)");
   if (rc == GROUT_OK) rc = hip_status(hipMemset(g->d_pos, 0, sizeof(uint32_t)), "hipMemset(position)");
-  if (rc == GROUT_OK)
-    rc = hip_status(hipStreamCreateWithFlags(&cap, hipStreamNonBlocking), "hipStreamCreate");
+  if (rc == GROUT_OK && cap == nullptr) {
+    rc = hip_status(hipStreamCreateWithFlags(&own, hipStreamNonBlocking), "hipStreamCreate");
+    cap = own;
+  }
   if (rc == GROUT_OK) {
     rc = hip_status(hipStreamBeginCapture(cap, hipStreamCaptureModeThreadLocal), "BeginCapture");
     if (rc == GROUT_OK) {
+      // Per layer: the fused norm/RoPE/KV write + split-K pass, then the merge.
       for (int i = 0; i < num_layers && rc == GROUT_OK; ++i) {
         const grout_decode_layer& L = layers[i];
-        rc = grout_qk_norm_rope_kv_decode(L.qkv, L.gamma_q, L.gamma_k, rope_cos, rope_sin,
-                                          L.q_rope, L.k_cache, L.v_cache, g->d_pos, num_q_heads,
-                                          num_kv_heads, head_dim, max_ctx, stride, eps, cap);
-        if (rc == GROUT_OK)
-          rc = grout_attn_decode(L.q_rope, L.k_cache, L.v_cache, L.attn_out, workspace,
-                                 workspace_bytes, g->d_pos, num_q_heads, num_kv_heads, head_dim,
-                                 max_ctx, stride, num_splits, qk_scale, cap);
+        rc = grout_attn_decode_fused(L.qkv, L.gamma_q, L.gamma_k, rope_cos, rope_sin, L.k_cache,
+                                     L.v_cache, L.attn_out, workspace, workspace_bytes, g->d_pos,
+                                     num_q_heads, num_kv_heads, head_dim, max_ctx, stride,
+                                     num_splits, eps, qk_scale, cap);
       }
       hipGraph_t graph = nullptr;
       const hipError_t e = hipStreamEndCapture(cap, &graph);
@@ -310,8 +313,7 @@ int grout_decode_graph_create(const grout_decode_layer* layers, int num_layers,
   if (rc == GROUT_OK)
     rc = hip_status(hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0),
                     "hipGraphInstantiate");
-  if (cap) (void)hipStreamDestroy(cap);
-  (void)stream;
+  if (own) (void)hipStreamDestroy(own);
   if (rc != GROUT_OK) {
     const std::string msg = g_last_error;
     grout_decode_graph_destroy(g);

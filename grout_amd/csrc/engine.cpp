@@ -21,6 +21,8 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <string>
@@ -139,6 +141,8 @@ struct grout_engine {
 
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
+  // Why decode runs without the graph ("" while the graph is in use).
+  std::string graph_error;
 
   int next_pos = 0;
   bool session_active = false;
@@ -331,6 +335,35 @@ int capture_decode_graph(grout_engine* e) {
                     "hipGraphInstantiate");
 }
 
+// The decode-step graph, or the sequential fallback: GROUT_HIP_GRAPH_DECODE=0
+// skips the capture, and a failed capture is reported on stderr and recorded
+// (src/model.rs:1700-1701, 2130-2145, 2300-2309).  Either way decode then
+// launches record_decode_step's kernels directly, in the same order.
+int setup_decode_graph(grout_engine* e) {
+  const char* env = std::getenv("GROUT_HIP_GRAPH_DECODE");
+  if (env && std::strcmp(env, "0") == 0) {
+    e->graph_error = "decode graph disabled by GROUT_HIP_GRAPH_DECODE=0";
+    return GROUT_OK;
+  }
+  if (capture_decode_graph(e) == GROUT_OK) return GROUT_OK;
+  e->graph_error = "decode graph capture failed: " + g_last_error;
+  std::fprintf(stderr, "grout: warning: %s; falling back to sequential decode\n",
+               e->graph_error.c_str());
+  (void)hipGetLastError();
+  if (e->exec) (void)hipGraphExecDestroy(e->exec);
+  if (e->graph) (void)hipGraphDestroy(e->graph);
+  e->exec = nullptr;
+  e->graph = nullptr;
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(e->stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone) {
+    hipGraph_t g = nullptr;
+    (void)hipStreamEndCapture(e->stream, &g);
+    if (g) (void)hipGraphDestroy(g);
+  }
+  // the stream must still work for the sequential path
+  return hip_status(hipStreamSynchronize(e->stream), "hipStreamSynchronize");
+}
+
 int ensure_prefill_capacity(grout_engine* e, int rows) {
   if (rows <= e->prefill_cap) return GROUT_OK;
   const auto& c = e->cfg;
@@ -408,7 +441,10 @@ int decode_common(grout_engine* e, uint32_t token) {
   set_step_kernel<<<1, 1, 0, e->stream>>>(e->d<uint32_t>(e->db.token), token,
                                           e->d<uint32_t>(e->db.pos), (uint32_t)e->next_pos);
   GROUT_CHECK(hip_status(hipGetLastError(), "set step"));
-  GROUT_CHECK(hip_status(hipGraphLaunch(e->exec, e->stream), "hipGraphLaunch"));
+  if (e->exec)
+    GROUT_CHECK(hip_status(hipGraphLaunch(e->exec, e->stream), "hipGraphLaunch"));
+  else
+    GROUT_CHECK(record_decode_step(e));
   e->next_pos += 1;
   return GROUT_OK;
 }
@@ -423,7 +459,8 @@ int validate_config(const grout_qwen3_config* c) {
   GROUT_NEED(c->intermediate_size >= 8 && c->intermediate_size % 8 == 0, GROUT_ENOTSUP,
              "intermediate_size=%d must be a positive multiple of 8", c->intermediate_size);
   GROUT_NEED(c->vocab_size >= 1, GROUT_EINVAL, "vocab_size=%d", c->vocab_size);
-  GROUT_NEED(c->max_ctx >= 1, GROUT_EINVAL, "max_ctx=%d", c->max_ctx);
+  GROUT_NEED(c->max_ctx >= 1 && c->max_ctx <= GROUT_MAX_CTX, GROUT_ENOTSUP,
+             "max_ctx=%d outside [1, %d]", c->max_ctx, GROUT_MAX_CTX);
   GROUT_NEED(std::isfinite(c->rms_norm_eps) && c->rms_norm_eps > 0.f, GROUT_EINVAL,
              "rms_norm_eps=%g", (double)c->rms_norm_eps);
   GROUT_NEED(std::isfinite(c->rope_theta) && c->rope_theta > 0.f, GROUT_EINVAL, "rope_theta=%g",
@@ -589,7 +626,34 @@ int create_impl(grout_engine* e, const grout_qwen3_config* c, const void* final_
   e->argmax_blocks = grout::argmax_num_blocks(c->vocab_size);
   e->qk_scale = 1.0f / std::sqrt(128.0f);  // src/model.rs:2654, 6901
 
+  // Decode buffers (offsets only until the preflight has passed).
+  const size_t H = c->hidden_size, I = c->intermediate_size, h2 = sizeof(uint16_t);
+  Arena a;
+  DecodeBufs& b = e->db;
+  b.hidden = a.take(H * h2);
+  b.normed = a.take(H * h2);
+  b.hidden_after_attn = a.take(H * h2);
+  b.qkv = a.take(e->qkv_dim * h2);
+  b.attn_out = a.take(e->q_dim * h2);
+  b.attn_proj = a.take(H * h2);
+  b.gate_up = a.take(2 * I * h2);
+  b.ff = a.take(I * h2);
+  b.ff_down = a.take(H * h2);
+  b.logits = a.take((size_t)c->vocab_size * h2);
+  b.argmax_max = a.take((size_t)e->argmax_blocks * sizeof(float));
+  b.argmax_idx = a.take((size_t)e->argmax_blocks * sizeof(uint32_t));
+  b.token = a.take(sizeof(uint32_t));
+  b.pos = a.take(sizeof(uint32_t));
+  b.workspace = a.take(e->ws_bytes);
+  e->deq_bytes = dequant_scratch_bytes(e);
+
   GROUT_CHECK(hip_status(hipSetDevice(device), "hipSetDevice"));
+  // VRAM preflight before the caches are allocated (src/model.rs:1491-1506);
+  // the caller's weights are resident already.
+  size_t free_b = 0, total_b = 0;
+  GROUT_CHECK(hip_status(hipMemGetInfo(&free_b, &total_b), "hipMemGetInfo"));
+  GROUT_CHECK(grout_engine_vram_preflight(c, 0, a.used + e->deq_bytes, free_b, total_b, nullptr));
+
   GROUT_CHECK(hip_status(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking),
                          "hipStreamCreate"));
   GROUT_CHECK(blas_status(rocblas_create_handle(&e->blas), "rocblas_create_handle"));
@@ -610,24 +674,6 @@ int create_impl(grout_engine* e, const grout_qwen3_config* c, const void* final_
                                    hipMemcpyHostToDevice),
                          "rope H2D"));
 
-  const size_t H = c->hidden_size, I = c->intermediate_size, h2 = sizeof(uint16_t);
-  Arena a;
-  DecodeBufs& b = e->db;
-  b.hidden = a.take(H * h2);
-  b.normed = a.take(H * h2);
-  b.hidden_after_attn = a.take(H * h2);
-  b.qkv = a.take(e->qkv_dim * h2);
-  b.attn_out = a.take(e->q_dim * h2);
-  b.attn_proj = a.take(H * h2);
-  b.gate_up = a.take(2 * I * h2);
-  b.ff = a.take(I * h2);
-  b.ff_down = a.take(H * h2);
-  b.logits = a.take((size_t)c->vocab_size * h2);
-  b.argmax_max = a.take((size_t)e->argmax_blocks * sizeof(float));
-  b.argmax_idx = a.take((size_t)e->argmax_blocks * sizeof(uint32_t));
-  b.token = a.take(sizeof(uint32_t));
-  b.pos = a.take(sizeof(uint32_t));
-  b.workspace = a.take(e->ws_bytes);
   GROUT_CHECK(hip_status(hipMalloc(&a.base, a.used), "hipMalloc(decode buffers)"));
   e->dec = a;
   GROUT_CHECK(hip_status(hipMemsetAsync(a.base, 0, a.used, e->stream), "hipMemset(decode)"));
@@ -638,11 +684,10 @@ int create_impl(grout_engine* e, const grout_qwen3_config* c, const void* final_
   GROUT_CHECK(hip_status(hipHostMalloc(reinterpret_cast<void**>(&e->h_token), sizeof(uint32_t),
                                        hipHostMallocDefault),
                          "hipHostMalloc(token)"));
-  e->deq_bytes = dequant_scratch_bytes(e);
   if (e->deq_bytes)
     GROUT_CHECK(hip_status(hipMalloc(&e->deq, e->deq_bytes), "hipMalloc(dequant scratch)"));
   GROUT_CHECK(hip_status(hipStreamSynchronize(e->stream), "hipStreamSynchronize"));
-  return capture_decode_graph(e);
+  return setup_decode_graph(e);
 }
 
 }  // namespace
@@ -714,6 +759,10 @@ static int check_gemv_norm(const void* W, const void* residual, const void* x,
   GROUT_CHECK(check_norm(1, k, eps));
   GROUT_CHECK(check_ptrs16({{W, "W"}, {x, "x"}, {gamma, "gamma"}}));
   if (residual) GROUT_CHECK(check_ptrs16({{residual, "residual"}, {residual_out, "residual_out"}}));
+  // One workgroup writes residual_out while the others still read residual
+  // and x: in-place use would race.
+  GROUT_NEED(residual_out == nullptr || (residual_out != residual && residual_out != x),
+             GROUT_EINVAL, "residual_out must not alias residual or x");
   GROUT_NEED(y != nullptr && (reinterpret_cast<uintptr_t>(y) & 1u) == 0, GROUT_EALIGN,
              "y is NULL or not 2-byte aligned");
   return GROUT_OK;
@@ -1035,6 +1084,38 @@ int grout_engine_reset(grout_engine* e) {
 
 int grout_engine_position(const grout_engine* e) { return e ? e->next_pos : -1; }
 
+int grout_engine_vram_preflight(const grout_qwen3_config* c, size_t weight_bytes,
+                                size_t scratch_bytes, size_t free_bytes, size_t total_bytes,
+                                size_t* required) {
+  GROUT_NEED(c != nullptr, GROUT_EINVAL, "config is NULL");
+  GROUT_NEED(c->num_layers >= 1 && c->num_kv_heads >= 1 && c->max_ctx >= 1, GROUT_EINVAL,
+             "num_layers=%d num_kv_heads=%d max_ctx=%d", c->num_layers, c->num_kv_heads,
+             c->max_ctx);
+  constexpr size_t kSlack = (size_t)700 << 20;  // src/model.rs:181
+  const size_t kv_per_token = (size_t)c->num_layers * c->num_kv_heads * 128 * 2 * sizeof(uint16_t);
+  const size_t kv = kv_per_token * (size_t)c->max_ctx;
+  const size_t rope = (size_t)c->max_ctx * 128 * sizeof(float);
+  const size_t need = weight_bytes + kv + rope + scratch_bytes + kSlack;
+  if (required) *required = need;
+  const double MiB = 1024.0 * 1024.0;
+  char summary[400];
+  std::snprintf(summary, sizeof(summary),
+                "max_ctx=%d: weights=%.1f MiB + KV=%d tokens * %.1f KiB/token = %.1f MiB + "
+                "rope=%.1f MiB + scratch=%.1f MiB + slack=%.1f MiB => required=%.1f MiB; "
+                "free=%.1f MiB / total=%.1f MiB",
+                c->max_ctx, weight_bytes / MiB, c->max_ctx, kv_per_token / 1024.0, kv / MiB,
+                rope / MiB, scratch_bytes / MiB, kSlack / MiB, need / MiB, free_bytes / MiB,
+                total_bytes / MiB);
+  GROUT_NEED(need <= free_bytes, GROUT_ENOMEM, "VRAM preflight failed: %s", summary);
+  return GROUT_OK;
+}
+
+int grout_engine_uses_decode_graph(const grout_engine* e) { return e && e->exec ? 1 : 0; }
+
+const char* grout_engine_decode_graph_error(const grout_engine* e) {
+  return e ? e->graph_error.c_str() : "";
+}
+
 int grout_engine_destroy(grout_engine* e) {
   if (!e) return GROUT_OK;
   if (e->stream) (void)hipStreamSynchronize(e->stream);
@@ -1057,7 +1138,26 @@ int grout_engine_destroy(grout_engine* e) {
 int grout_engine_load(const char* model_dir, int max_ctx, int device, grout_engine** out) {
   GROUT_NEED(out != nullptr, GROUT_EINVAL, "out is NULL");
   *out = nullptr;
-  GROUT_NEED(max_ctx >= 0, GROUT_EINVAL, "max_ctx=%d", max_ctx);
+  GROUT_NEED(max_ctx >= 0 && max_ctx <= GROUT_MAX_CTX, GROUT_EINVAL,
+             "max_ctx=%d outside [0, %d]", max_ctx, GROUT_MAX_CTX);
+  // VRAM preflight with the model's weights before any of them is uploaded
+  // (src/model.rs:1491-1506); create repeats it for the engine's own state.
+  {
+    grout_model_info pre{};
+    GROUT_CHECK(grout_model_inspect(model_dir, &pre));
+    grout_qwen3_config pc = pre.config;
+    if (max_ctx > 0) pc.max_ctx = max_ctx;
+    GROUT_NEED(pc.max_ctx >= 1 && pc.max_ctx <= GROUT_MAX_CTX, GROUT_ENOTSUP,
+               "max_position_embeddings=%d exceeds GROUT_MAX_CTX=%d: pass a smaller max_ctx",
+               pc.max_ctx, GROUT_MAX_CTX);
+    int ndev = 0;
+    GROUT_CHECK(hip_status(hipGetDeviceCount(&ndev), "hipGetDeviceCount"));
+    GROUT_NEED(device >= 0 && device < ndev, GROUT_EINVAL, "device %d of %d", device, ndev);
+    GROUT_CHECK(hip_status(hipSetDevice(device), "hipSetDevice"));
+    size_t free_b = 0, total_b = 0;
+    GROUT_CHECK(hip_status(hipMemGetInfo(&free_b, &total_b), "hipMemGetInfo"));
+    GROUT_CHECK(grout_engine_vram_preflight(&pc, pre.weight_bytes, 0, free_b, total_b, nullptr));
+  }
   grout_model* m = nullptr;
   GROUT_CHECK(grout_model_load(model_dir, device, &m));
   grout_model_info info;

@@ -93,8 +93,9 @@ class AttentionEngine:
 
 class DecodeGraph:
     """HIP graph of the attention part of one decode step over all layers:
-    per layer fused norm/RoPE/KV write -> split-K decode -> merge.  Callers
-    write each layer's QKV projection into `qkv[layer]` and read `attn_out[layer]`."""
+    per layer the fused norm/RoPE/KV write + split-K pass, then the merge
+    (grout_attn_decode_fused).  Callers write each layer's QKV projection
+    into `qkv[layer]` and read `attn_out[layer]`."""
 
     def __init__(self, eng: AttentionEngine, num_splits: Optional[int] = None):
         cfg = eng.cfg
@@ -104,15 +105,13 @@ class DecodeGraph:
         self.num_splits = num_splits or ops.default_splits(cfg.max_ctx, Hq, Hkv)
         self.qkv = [torch.zeros((Hq + 2 * Hkv) * D, dtype=torch.float16, device=dev)
                     for _ in range(cfg.num_layers)]
-        self.q_rope = [torch.zeros((Hq, D), dtype=torch.float16, device=dev)
-                       for _ in range(cfg.num_layers)]
         self.attn_out = [torch.zeros((Hq, D), dtype=torch.float16, device=dev)
                          for _ in range(cfg.num_layers)]
         self.workspace = ops.decode_workspace(Hq, Hkv, self.num_splits, dev)
         layers = (DecodeLayer * cfg.num_layers)()
         for i in range(cfg.num_layers):
             layers[i] = DecodeLayer(self.qkv[i].data_ptr(), eng.q_norm[i].data_ptr(),
-                                    eng.k_norm[i].data_ptr(), self.q_rope[i].data_ptr(),
+                                    eng.k_norm[i].data_ptr(), None,
                                     eng.k_caches[i].data_ptr(), eng.v_caches[i].data_ptr(),
                                     self.attn_out[i].data_ptr())
         handle = C.c_void_p()

@@ -480,6 +480,17 @@ class Engine:
     def position(self) -> int:
         return int(lib().grout_engine_position(self._h))
 
+    @property
+    def uses_decode_graph(self) -> bool:
+        """True when decode replays the captured decode-step graph."""
+        return bool(lib().grout_engine_uses_decode_graph(self._h))
+
+    @property
+    def decode_graph_error(self) -> str:
+        """Why decode runs the sequential fallback ("" with the graph);
+        GenerationOutput::decode_graph_error (src/model.rs:1359)."""
+        return (lib().grout_engine_decode_graph_error(self._h) or b"").decode()
+
     # -- src/api.rs:162-170
     def warmup(self) -> None:
         tok = self._meta.eos_token_ids[0] if self._meta.eos_token_ids else 0

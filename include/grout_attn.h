@@ -34,6 +34,11 @@ extern "C" {
 #define GROUT_EALIGN (-2)   /* pointer or stride not 16-byte aligned    */
 #define GROUT_ENOTSUP (-3)  /* configuration this build does not handle */
 
+/* Largest cache length (max_ctx, or pos0 + seq_len for prefill) any entry
+ * point accepts: the kernels address cache rows and rope-table rows with
+ * 32-bit byte offsets. */
+#define GROUT_MAX_CTX (1 << 22)
+
 /* Message of the last failing call on this thread ("" if none). */
 const char* grout_last_error(void);
 
@@ -172,7 +177,7 @@ typedef struct grout_decode_layer {
   const void* qkv;      /* [(Hq+2Hkv)*128] fp16 input of the fused norm/RoPE/KV write */
   const void* gamma_q;  /* [128] fp16 */
   const void* gamma_k;  /* [128] fp16 */
-  void* q_rope;         /* [Hq][128] fp16 scratch: rotated q */
+  void* q_rope;         /* unused (the rotated q rows stay on chip); may be NULL */
   void* k_cache;        /* [Hkv][max_ctx][128] fp16 */
   void* v_cache;        /* [Hkv][max_ctx][128] fp16 */
   void* attn_out;       /* [Hq][128] fp16 */
@@ -180,13 +185,19 @@ typedef struct grout_decode_layer {
 
 typedef struct grout_decode_graph grout_decode_graph;
 
-/* Captures, on `stream`, num_layers x [fused norm/RoPE/KV write -> split-K
- * decode -> merge] into one HIP graph.  The graph reads the position from
- * its own device word, written by grout_decode_graph_launch; `workspace`
+/* Captures num_layers x grout_attn_decode_fused (the fused norm/RoPE/KV
+ * write + split-K pass, then the merge: two launches per layer, one with a
+ * single split) into one HIP graph.  The capture runs on `stream`, or on a
+ * private stream when `stream` is NULL (the legacy stream cannot be
+ * captured); nothing is executed on `stream` by this call.  Creation is not
+ * a hot call: it allocates the graph's device position word (hipMalloc) and
+ * zeroes it synchronously before the capture.  The graph reads the position
+ * from that word, written by grout_decode_graph_launch; `workspace`
  * (grout_attn_decode_workspace_bytes(..., num_splits)) is shared by the
  * layers, which run in order.  num_splits <= 0 picks the default for max_ctx.
  * Replaces DecodeCudaGraphRunner / build_decode_graph_scope
- * (src/model.rs:408-596, 2631-4006) for the attention records. */
+ * (src/model.rs:408-596, 2631-4006) for the attention records
+ * (src/model.rs:3492-3519, 3713-3771). */
 int grout_decode_graph_create(const grout_decode_layer* layers, int num_layers,
                               const float* rope_cos, const float* rope_sin, void* workspace,
                               size_t workspace_bytes, int num_q_heads, int num_kv_heads,

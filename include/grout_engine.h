@@ -31,6 +31,7 @@ extern "C" {
 #endif
 
 #define GROUT_EBLAS (-4) /* a rocBLAS call of the prefill failed (message in grout_last_error) */
+#define GROUT_ENOMEM (-5) /* VRAM preflight: the engine would not fit in free device memory */
 
 /* The Qwen3Config fields the engine reads (src/config.rs:7-33). */
 typedef struct grout_qwen3_config {
@@ -239,11 +240,17 @@ int grout_model_get_info(const grout_model* model, grout_model_info* info);
 int grout_model_weights(const grout_model* model, grout_qwen3_weights* weights);
 int grout_model_free(grout_model* model);
 
-/* Validates the configuration and every weight pointer, allocates the
+/* Validates the configuration and every weight pointer, runs the VRAM
+ * preflight (grout_engine_vram_preflight with weight_bytes = 0: the caller's
+ * weights are resident already) against hipMemGetInfo, allocates the
  * engine's device state on `device` and captures the decode-step graph.
  * Mirrors Engine::load (src/api.rs:60-90) minus the file loading, with the
  * graph capture of DecodeCudaGraphRunner (src/model.rs:408-596,
- * 2631-4006). */
+ * 2631-4006).  With GROUT_HIP_GRAPH_DECODE=0 in the environment, or when the
+ * capture fails (a warning goes to stderr), the engine is still created and
+ * decode launches the same step's kernels one by one on the engine's stream
+ * (the reference's sequential fallback, src/model.rs:2130-2145, 2300-2309);
+ * grout_engine_decode_graph_error says which. */
 int grout_engine_create(const grout_qwen3_config* config, const grout_qwen3_weights* weights,
                         int device, grout_engine** out);
 
@@ -281,10 +288,13 @@ typedef struct {
   const grout_qwen3_qlayer* layers;     /* num_layers entries */
 } grout_qwen3_qweights;
 
-/* grout_engine_create over mixed-format weights.  Decode: the norms as their
- * own kernels, then the low-bit GEMV per part (gate_up as one part: SiLU in
- * the GEMV epilogue), f16 parts as in grout_engine_create; the embedding row
- * is gathered from the table.  Prefill and extend: each low-bit part is
+/* grout_engine_create over mixed-format weights.  Decode: every qkv and
+ * gate_up part runs the low-bit GEMV with the input / post-attention RMSNorm
+ * folded in (grout_gemv_q_rms_norm; each part recomputes the norm and writes
+ * the same residual bits), gate_up as one part with SiLU(gate) * up in the
+ * epilogue (grout_gemv_q_rms_norm_silu_mul), o / down / lm_head the plain
+ * low-bit GEMV, f16 parts as in grout_engine_create; the embedding row is
+ * gathered from the table.  Prefill and extend: each low-bit part is
  * dequantized to f16 into an engine scratch buffer and multiplied with the
  * GEMM (the reference's prefill dequant scratch, src/quant_scratch.rs:17-105).
  * Every part's format must fit its k (grout_qweight_bytes != 0). */
@@ -296,10 +306,12 @@ int grout_engine_create_q(const grout_qwen3_config* config, const grout_qwen3_qw
  * way round).  Valid until grout_model_free. */
 int grout_model_qweights(const grout_model* model, grout_qwen3_qweights* weights);
 
-/* Engine::load (src/api.rs:60-90): grout_model_load + grout_engine_create
- * (grout_engine_create_q for a .gguf path)
- * with max_ctx (0 = max_position_embeddings); the engine owns the model and
- * frees it in grout_engine_destroy. */
+/* Engine::load (src/api.rs:60-90): grout_model_inspect, the VRAM preflight
+ * with the model's weight bytes (before any weight is uploaded, as
+ * src/model.rs:1491-1506), grout_model_load + grout_engine_create
+ * (grout_engine_create_q for a .gguf path) with max_ctx
+ * (0 = max_position_embeddings, which must then be <= GROUT_MAX_CTX); the
+ * engine owns the model and frees it in grout_engine_destroy. */
 int grout_engine_load(const char* model_dir, int max_ctx, int device, grout_engine** out);
 
 /* Info of the model an engine was loaded from (GROUT_EINVAL for engines made
@@ -327,7 +339,8 @@ int grout_engine_extend(grout_engine* engine, const uint32_t* tokens, int n_toke
                         float* logits_out, uint32_t* next_token);
 
 /* Decodes `token` at the next position of the session (one replay of the
- * decode-step graph) and writes next-token logits (f32, vocab_size floats).
+ * decode-step graph, or the same kernels launched one by one without it)
+ * and writes next-token logits (f32, vocab_size floats).
  * Requires a preceding prefill and position < max_ctx.
  * Mirrors Engine::decode (src/api.rs:110-121). */
 int grout_engine_decode(grout_engine* engine, uint32_t token, float* logits_out);
@@ -342,6 +355,28 @@ int grout_engine_decode_greedy(grout_engine* engine, uint32_t token, uint32_t* n
  * and reported by the next call.  Mirrors Engine::reset (src/api.rs:139-154)
  * and the in-place cache reset (src/model.rs:536-565). */
 int grout_engine_reset(grout_engine* engine);
+
+/* Host only.  Device bytes an engine for `config` needs besides what the
+ * caller already holds: weight_bytes (the model's, when they are still to be
+ * uploaded; 0 for caller-owned weights) + the K/V caches
+ * (num_layers * 2 * Hkv * max_ctx * 128 * 2 B) + the RoPE tables
+ * (max_ctx * 128 * 4 B) + scratch_bytes (decode buffers, prefill dequant
+ * scratch) + 700 MiB of slack, written to *required (may be NULL).  Returns
+ * GROUT_ENOMEM, with the itemized summary in grout_last_error(), when that
+ * exceeds free_bytes.  Mirrors run_vram_preflight (src/model.rs:345-380). */
+int grout_engine_vram_preflight(const grout_qwen3_config* config, size_t weight_bytes,
+                                size_t scratch_bytes, size_t free_bytes, size_t total_bytes,
+                                size_t* required);
+
+/* 1 when decode replays the captured decode-step graph, 0 when it runs the
+ * sequential fallback (or engine is NULL). */
+int grout_engine_uses_decode_graph(const grout_engine* engine);
+
+/* Why decode runs the sequential fallback: the capture error, or the
+ * GROUT_HIP_GRAPH_DECODE=0 setting; "" when the graph is in use.  Mirrors
+ * GenerationOutput::decode_graph_error (src/model.rs:1359).  Valid until
+ * grout_engine_destroy. */
+const char* grout_engine_decode_graph_error(const grout_engine* engine);
 
 /* Position the next decode writes (number of tokens in the session). */
 int grout_engine_position(const grout_engine* engine);

@@ -120,3 +120,63 @@ def test_ops_fail_loudly_without_library(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "missing.so"))
     with pytest.raises(RuntimeError, match="missing"):
         _lib.lib()
+
+
+def _cfg4b(max_ctx):
+    return _lib.Qwen3Config(36, 2560, 9728, 32, 8, 128, 151936, 1e-6, 1e6, max_ctx)
+
+
+def test_vram_preflight_sums_and_refuses_without_gpu():
+    """The preflight's byte total and its refusal are host arithmetic: KV is
+    layers x 2 x Hkv x max_ctx x 256 B, rope max_ctx x 512 B, plus weights,
+    scratch and 700 MiB of slack (src/model.rs:181, 345-380)."""
+    L = grout_amd.lib()
+    cfg = _cfg4b(32768)
+    req = _lib._sz(0)
+    kv = 36 * 2 * 8 * 32768 * 128 * 2
+    rope = 32768 * 128 * 4
+    slack = 700 << 20
+    w, scr = 8_044_936_192, 123_456
+    assert L.grout_engine_vram_preflight(C.byref(cfg), w, scr, 1 << 40, 1 << 40, C.byref(req)) == 0
+    assert req.value == w + kv + rope + scr + slack
+    # one byte short of the requirement -> GROUT_ENOMEM with the itemized summary
+    rc = L.grout_engine_vram_preflight(C.byref(cfg), w, scr, req.value - 1, 1 << 40, None)
+    assert rc == -5
+    msg = _lib.last_error()
+    assert "VRAM preflight failed" in msg and "max_ctx=32768" in msg and "KV=32768 tokens" in msg
+    assert L.grout_engine_vram_preflight(C.byref(cfg), w, scr, req.value, 1 << 40, None) == 0
+    assert L.grout_engine_vram_preflight(None, 0, 0, 0, 0, None) == -1
+
+
+def test_max_ctx_cap_and_engine_queries_without_gpu():
+    L = grout_amd.lib()
+    keep, p = _aligned()
+    # cache lengths past GROUT_MAX_CTX (32-bit row offsets) are refused up front
+    big = (1 << 22) + 1
+    rc = L.grout_attn_decode(p, p, p, p, p, 1 << 20, p, 8, 2, 128, big, big * 128, 4, 0.088, None)
+    assert rc == -3 and "GROUT_MAX_CTX" in _lib.last_error()
+    rc = L.grout_fmha_prefill(p, p, p, p, 8, (1 << 22) - 4, 8, 2, 128, big * 128, 0.088, None)
+    assert rc == -3 and "GROUT_MAX_CTX" in _lib.last_error()
+    # engine status queries on NULL
+    assert L.grout_engine_uses_decode_graph(None) == 0
+    assert L.grout_engine_decode_graph_error(None) == b""
+    # an engine config past the cap is refused before any device call
+    cfg = _cfg4b(big)
+    h = C.c_void_p()
+    w = _lib.Qwen3Weights()
+    assert L.grout_engine_create(C.byref(cfg), C.byref(w), 0, C.byref(h)) in (-1, -3)
+
+
+def test_gemv_norm_rejects_residual_aliasing_without_gpu():
+    """The norm-folded GEMV's first workgroup writes residual_out while the
+    others still read residual and x: in-place use is refused."""
+    L = grout_amd.lib()
+    keep, p = _aligned(1 << 16)
+    a = C.c_void_p(p.value + 4096)
+    b = C.c_void_p(p.value + 8192)
+    for fn in ("grout_gemv_rms_norm", "grout_gemv_rms_norm_silu_mul"):
+        f = getattr(L, fn)
+        assert f(p, a, b, p, a, p, 16, 64, 1e-6, None) == -1  # residual_out == residual
+        assert "alias" in _lib.last_error()
+        assert f(p, a, b, p, b, p, 16, 64, 1e-6, None) == -1  # residual_out == x
+        assert "alias" in _lib.last_error()

@@ -109,6 +109,7 @@ def _decode_case(gpu, Hq, Hkv, ctx, max_ctx, num_splits, tag):
     (32, 8, 4096, 32768, 7),
     (32, 8, 4096, 32768, 200),    # more splits than tiles: empty splits
     (64, 8, 8192, 32768, None),   # config 4 (32B)
+    (64, 8, 16384, 32768, None),
     (64, 8, 32768, 32768, None),
     (8, 8, 1, 64, None),          # ctx = 1, G = 1
     (32, 2, 100, 160, 3),         # ragged ctx, G = 16
@@ -126,6 +127,7 @@ def test_decode_attention_vs_oracle(gpu, Hq, Hkv, ctx, max_ctx, splits):
     (32, 8, 640, 1024, None),     # default splits + merge
     (32, 8, 4095, 4096, 1),
     (64, 8, 8191, 32768, None),   # 32B, G = 8
+    (64, 8, 16383, 32768, None),  # config 4 at ctx 16384
     (32, 2, 100, 160, 3),         # G = 16, ragged
     (40, 8, 16, 64, 1),           # G = 5, the new row opens a tile
     (8, 8, 0, 64, 1),             # first position
@@ -285,11 +287,12 @@ def test_config1_decode_step_pipeline(gpu):
     assert_close(host_f32(out).reshape(Hq, D), out_ref, "config1 decode step")
 
 
-@pytest.mark.parametrize("S", [512, 2048])
+@pytest.mark.parametrize("S", [512, 2048, 8192])
 def test_config3_prefill_pipeline(gpu, S):
     """Qwen3-4B-shaped prefill: fused QK-norm/RoPE/KV write at positions
-    0..S-1, then causal FMHA.  S=512 checked in full; S=2048 on rows 0..63,
-    the last 64 rows and 64 seeded random rows."""
+    0..S-1, then causal FMHA.  S=512 checked in full; S=2048 and S=8192 on
+    rows 0..63, the last 64 rows and 64 seeded random rows (every head of
+    each row); rotated q and the K/V cache rows in full, bit for bit."""
     _say("config3", S)
     Hq, Hkv, max_ctx = 32, 8, 32768
     q, k, v = normal(f"c3q{S}", (S, Hq, D)), normal(f"c3k{S}", (S, Hkv, D)), normal(f"c3v{S}", (S, Hkv, D))

@@ -391,6 +391,52 @@ def test_engine_greedy_matches_logits_and_reset_is_clean(gpu):
         eng.close()
 
 
+def test_engine_sequential_decode_fallback_matches_graph(gpu, monkeypatch):
+    """GROUT_HIP_GRAPH_DECODE=0 (and a failed capture) leaves decode on the
+    sequential path, which launches the graph's kernels in the same order:
+    logits equal the graph's bit for bit (src/model.rs:2130-2145)."""
+    cfg = tiny_configs()["g2"]
+    host_w = Q.random_host_weights(cfg, seed=4, std=0.05)
+    prompt = [3, 1, 4, 1, 5, 9, 2, 6]
+    eng = make_engine(cfg, host_w, 32)
+    monkeypatch.setenv("GROUT_HIP_GRAPH_DECODE", "0")
+    seq = make_engine(cfg, host_w, 32)
+    try:
+        assert eng.uses_decode_graph and eng.decode_graph_error == ""
+        assert not seq.uses_decode_graph
+        assert "GROUT_HIP_GRAPH_DECODE=0" in seq.decode_graph_error
+        a, b = eng.prefill(prompt).values, seq.prefill(prompt).values
+        assert np.array_equal(a, b)
+        tok = int(np.argmax(a))
+        for i in range(6):
+            la, lb = eng.decode(tok).values, seq.decode(tok).values
+            assert np.array_equal(la, lb), f"decode step {i}"
+            tok = int(np.argmax(la))
+        assert seq.decode_greedy(tok) == eng.decode_greedy(tok)
+    finally:
+        eng.close()
+        seq.close()
+
+
+def test_engine_vram_preflight_refuses_before_allocating(gpu):
+    """36 layers x 8 kv heads at max_ctx 2^22 need 604 GB of K/V: the
+    preflight (src/model.rs:345-380) refuses with GROUT_ENOMEM and the
+    itemized summary before any device allocation."""
+    import torch
+    from grout_amd._lib import GroutError
+    from grout_amd.model import Qwen3Config
+
+    cfg = Qwen3Config(num_layers=36, hidden_size=256, intermediate_size=512,
+                      num_attention_heads=32, num_key_value_heads=8, vocab_size=300)
+    host_w = Q.random_host_weights(cfg, seed=9, std=0.05)
+    free0, _ = torch.cuda.mem_get_info()
+    with pytest.raises(GroutError, match="VRAM preflight failed") as ei:
+        make_engine(cfg, host_w, 1 << 22)
+    assert ei.value.code == -5 and "KV=4194304 tokens" in str(ei.value)
+    free1, _ = torch.cuda.mem_get_info()
+    assert abs(free1 - free0) < (64 << 20)
+
+
 def test_engine_argument_errors(gpu):
     from grout_amd._lib import GroutError
 
