@@ -83,6 +83,7 @@ SIGNATURES = {
     "grout_attn_decode_default_splits": (_i, [_i, _i, _i]),
     "grout_attn_decode_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "grout_attn_decode": (_i, [_p, _p, _p, _p, _p, _sz, _p, _i, _i, _i, _i, _l, _i, _f, _p]),
+    "grout_attn_decode_noalloc": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _i, _l, _i, _f, _p]),
     "grout_fmha_decode_gqa_split": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _l, _i, _f, _p]),
     "grout_splitk_reduce_merge": (_i, [_p, _p, _p, _i, _i, _i, _i, _p]),
     "grout_attn_decode_fused": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p, _i, _i, _i, _i,

@@ -5,6 +5,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 
@@ -237,6 +238,83 @@ int grout_attn_decode_fused(const void* qkv, const void* gamma_q, const void* ga
                                                     num_splits, eps, qk_scale, part_acc, part_ml,
                                                     out, as_stream(stream)),
                     "attn_decode_fused launch");
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------- no-allocation decode
+//
+// grout_attn_decode_noalloc keeps the split partials in this file-scope
+// device array instead of a caller workspace.  In host code `scratch` only
+// names the symbol: its device address (one per GPU) comes from
+// hipGetSymbolAddress, looked up once per device with that device current,
+// and only that address is passed to kernels.
+namespace {
+
+static __device__ __align__(256) unsigned char scratch[GROUT_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+// Device address of `scratch` on the device `stream` belongs to.
+int noalloc_scratch(hipStream_t stream, void** out) {
+  int cur = 0;
+  GROUT_CHECK(hip_status(hipGetDevice(&cur), "hipGetDevice"));
+  int dev = cur;
+  if (stream != nullptr) GROUT_CHECK(hip_status(hipStreamGetDevice(stream, &dev), "hipStreamGetDevice"));
+  GROUT_NEED(dev >= 0 && dev < kMaxDevices, GROUT_ENOTSUP, "device %d >= %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    if (dev != cur) GROUT_CHECK(hip_status(hipSetDevice(dev), "hipSetDevice"));
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) (void)hipSetDevice(cur);
+    GROUT_CHECK(hip_status(e, "hipGetSymbolAddress(scratch)"));
+    GROUT_NEED(p != nullptr, GROUT_EINVAL, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return GROUT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int grout_attn_decode_noalloc(const void* q, const void* k_cache, const void* v_cache, void* out,
+                              const uint32_t* d_pos, int num_q_heads, int num_kv_heads,
+                              int head_dim, int max_ctx, long kv_head_stride, int num_splits,
+                              float qk_scale, void* stream) {
+  GROUT_CHECK(check_heads(num_q_heads, num_kv_heads, head_dim, kMaxDecodeGroup));
+  if (num_splits <= 0) num_splits = grout_attn_decode_default_splits(max_ctx, num_q_heads, num_kv_heads);
+  GROUT_NEED(num_splits <= kMaxSplits, GROUT_EINVAL, "num_splits=%d > %d", num_splits, kMaxSplits);
+  GROUT_NEED(max_ctx >= 1, GROUT_EINVAL, "max_ctx=%d", max_ctx);
+  GROUT_NEED(std::isfinite(qk_scale) && qk_scale > 0.f, GROUT_EINVAL, "qk_scale=%g",
+             (double)qk_scale);
+  GROUT_NEED(d_pos != nullptr, GROUT_EINVAL, "d_pos is NULL");
+  const size_t need = decode_ws_bytes(num_q_heads, num_kv_heads, num_splits);
+  GROUT_NEED(need <= (size_t)GROUT_NOALLOC_SCRATCH_BYTES, GROUT_EINVAL,
+             "%d splits need %zu bytes of scratch, more than the %d-byte static scratch of "
+             "grout_attn_decode_noalloc (use fewer splits, or grout_attn_decode)",
+             num_splits, need, GROUT_NOALLOC_SCRATCH_BYTES);
+  GROUT_CHECK(check_ptrs16({{q, "q"}, {k_cache, "k_cache"}, {v_cache, "v_cache"}, {out, "out"}}));
+  GROUT_CHECK(check_stride(kv_head_stride, max_ctx));
+  void* ws = nullptr;
+  GROUT_CHECK(noalloc_scratch(as_stream(stream), &ws));
+  // Every split workgroup writes all of its partials (empty splits write a
+  // zero sum), so the merge never reads a value left by an earlier call.
+  float* part_acc = static_cast<float*>(ws);
+  const size_t G = (size_t)(num_q_heads / num_kv_heads);
+  float* part_ml = part_acc + (size_t)num_kv_heads * num_splits * G * 128;
+  GROUT_CHECK(hip_status(grout::launch_attn_decode_split(q, k_cache, v_cache, kv_head_stride,
+                                                         d_pos, max_ctx, num_q_heads, num_kv_heads,
+                                                         num_splits, qk_scale, part_acc, part_ml,
+                                                         as_stream(stream)),
+                         "attn_decode_noalloc split launch"));
+  return hip_status(grout::launch_attn_decode_merge(part_acc, part_ml, out, num_q_heads,
+                                                    num_kv_heads, num_splits, as_stream(stream)),
+                    "attn_decode_noalloc merge launch");
 }
 
 // ------------------------------------------------------------------ graph

@@ -134,6 +134,26 @@ int grout_attn_decode(const void* q, const void* k_cache, const void* v_cache, v
                       int num_q_heads, int num_kv_heads, int head_dim, int max_ctx,
                       long kv_head_stride, int num_splits, float qk_scale, void* stream);
 
+/* Bytes of the static device scratch of grout_attn_decode_noalloc (per GPU). */
+#define GROUT_NOALLOC_SCRATCH_BYTES (4 << 20)
+
+/* grout_attn_decode without a workspace and without any allocation.  No
+ * counterpart in the reference: this entry point is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The split partials live in a static
+ * device array of GROUT_NOALLOC_SCRATCH_BYTES (4 MiB) that each GPU the
+ * library runs on holds until the process ends; a call whose
+ * grout_attn_decode_workspace_bytes(..., num_splits) exceeds that fails with
+ * GROUT_EINVAL before launching.  The first call on a device looks the array's
+ * address up (hipGetSymbolAddress); make that first call outside graph
+ * capture.  Every call on one GPU shares its array: calls that overlap in
+ * time on one GPU (other streams, other threads) race.  Output is
+ * bit-identical to grout_attn_decode's with the same num_splits. */
+int grout_attn_decode_noalloc(const void* q, const void* k_cache, const void* v_cache, void* out,
+                              const uint32_t* d_pos, int num_q_heads, int num_kv_heads,
+                              int head_dim, int max_ctx, long kv_head_stride, int num_splits,
+                              float qk_scale, void* stream);
+
 /* The two halves of grout_attn_decode, for callers that schedule them
  * separately (the reference records them as two kernels).  part_acc
  * [Hkv][splits][G][128] fp32 unnormalized, part_ml [Hkv][splits][G][2] fp32
