@@ -101,4 +101,67 @@ __device__ __forceinline__ u32x2 norm_rope_row(u32x2 xr, half4 gh, floatx4 c, fl
   return __builtin_bit_cast(u32x2, y);
 }
 
+// The same row on an 8-lane group (8 rows per wave): lane i (0..7) owns
+// elements 8i..8i+7 ("lo", x16 bytes 16i..) and their RoPE partners
+// 8i+64..8i+71 ("hi", bytes 128+16i..), so the rotation needs no exchange.
+// The sum of squares pairs exactly as in norm_rope_row (and the CPU
+// restatement): with group g = elements 4g..4g+3, lane i holds groups 2i,
+// 2i+1 (lo) and 2i+16, 2i+17 (hi); the butterfly's distance-16 step adds them
+// in-lane, distances 8, 4 and 2 are lanes i^4, i^2, i^1, distance 1 adds the
+// two lane values.  IEEE addition commutes, so every sum equals the 32-lane
+// tree's bit for bit.  All 8 lanes of the group must be active.
+__device__ __forceinline__ float xor_lane4(float x) {
+  // ds_swizzle bitmask mode: and 0x1f, or 0, xor 4
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x101f));
+}
+__device__ __forceinline__ float xor_lane2(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4e, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float xor_lane1(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xb1, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ void norm_rope_row8(u32x4 xlo, u32x4 xhi, half8 glo, half8 ghi,
+                                               const float (&c)[8], const float (&sn)[8],
+                                               float eps, u32x4& ylo, u32x4& yhi) {
+#pragma clang fp contract(off)
+  const half8 l = __builtin_bit_cast(half8, xlo), hh = __builtin_bit_cast(half8, xhi);
+  float xl[8], xh[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    xl[e] = (float)l[e];
+    xh[e] = (float)hh[e];
+  }
+  auto grp = [](const float* x) {
+    const float a = x[0] * x[0], b = x[1] * x[1], cc = x[2] * x[2], d = x[3] * x[3];
+    const float s0 = a + b, s1 = cc + d;
+    return s0 + s1;
+  };
+  // distance 16: group 2i + group 2i+16, group 2i+1 + group 2i+17
+  float u0 = grp(xl) + grp(xh);
+  float u1 = grp(xl + 4) + grp(xh + 4);
+  u0 = u0 + xor_lane4(u0);
+  u1 = u1 + xor_lane4(u1);
+  u0 = u0 + xor_lane2(u0);
+  u1 = u1 + xor_lane2(u1);
+  u0 = u0 + xor_lane1(u0);
+  u1 = u1 + xor_lane1(u1);
+  const float ss = u0 + u1;
+  const float mean = ss / (float)kHeadDim;
+  const float inv = rsqrt_det(mean + eps);
+
+  half8 yl, yh;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float nl = (xl[e] * inv) * (float)glo[e];
+    const float nh = (xh[e] * inv) * (float)ghi[e];
+    const float a = nl * c[e], b = nh * sn[e];
+    yl[e] = (half_t)(a - b);
+    const float f = nh * c[e], g = nl * sn[e];
+    yh[e] = (half_t)(f + g);
+  }
+  ylo = __builtin_bit_cast(u32x4, yl);
+  yhi = __builtin_bit_cast(u32x4, yh);
+}
+
 }  // namespace grout
