@@ -154,7 +154,9 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const half_t* __restrict_
 // then all R x CH weight reads (16 bytes per lane each, HBM), and only then
 // computes: the norm of the input overlaps the weight stream, and every wave
 // has its whole share of HBM reads in flight at once.  Partial sums meet in a
-// wave reduction (no LDS, no barrier); waves are independent.  The decode
+// wave reduction; with a plain input the waves are independent (no LDS, no
+// barrier), with a norm input the workgroup shares x' through LDS
+// (gemv_norm_lds_kernel).  The decode
 // shapes compile with CH = the exact chunk count, so no branch separates the
 // loads (a branch there makes the compiler wait for every outstanding load
 // before issuing the next); other K loop over batches of 8 chunks.
@@ -362,6 +364,132 @@ __device__ __forceinline__ void gemv_loop(const half_t* __restrict__ W, const Ge
   gemv_store<R, OUT>(acc, y, gwave, N, lane);
 }
 
+// Norm inputs (kNorm / kAddNorm) with exactly CH chunks: the kNormWaves waves
+// of a workgroup compute x' once, into LDS, instead of every wave re-reading
+// x, residual and gamma and redoing the norm (for two rows per wave that was
+// 1.5 input bytes through L1 per weight byte).  Each thread loads its share
+// of the inputs, then its wave's R x CH weight reads are issued, so the norm
+// (two barriers) overlaps the weight stream as before.  R weight rows per
+// wave; kSiluPairs: R / 2 (gate, up) pairs.  Measured on MI355X at the
+// Qwen3-4B shapes (HIP events, rotating weights): QKV 6144 x 2560 6.95 vs
+// 7.83 us, gate_up 19456 x 2560 16.4 vs 20.9 us.
+constexpr int kNormWaves = 4;
+
+template <int R, int IN, int OUT, int CH>
+__global__ __launch_bounds__(kNormWaves * 64) void gemv_norm_lds_kernel(
+    const half_t* __restrict__ W, GemvArgs a, half_t* __restrict__ y, int N, int K) {
+  constexpr int T = kNormWaves * 64;
+  constexpr int NV = (CH * 64 + T - 1) / T;  // input vectors (8 halves) per thread
+  constexpr int P = OUT == kSiluPairs ? R / 2 : R;  // outputs per wave
+  __shared__ __attribute__((aligned(16))) half_t s_x[CH * 512];
+  __shared__ float s_ss[kNormWaves];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int gwave = blockIdx.x * kNormWaves + w;
+  // weight rows (clamped for the loads; waves past N still join the barriers)
+  const half_t* wrow[R];
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const int o = gwave * P + i;
+    const int oc = o < N ? o : N - 1;
+    if (OUT == kSiluPairs) {
+      wrow[2 * i] = W + (size_t)oc * K;
+      wrow[2 * i + 1] = W + (size_t)(N + oc) * K;
+    } else {
+      wrow[i] = W + (size_t)oc * K;
+    }
+  }
+  // 1. input reads: vector v = threadIdx.x + T i covers k = 8v .. 8v+7
+  u32x4 xa[NV], xr[NV], xg[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int v = threadIdx.x + T * i;
+    const int kk = v < CH * 64 && 8 * v < K ? 8 * v : 0;
+    xa[i] = load16(a.x + kk);
+    if (IN == kAddNorm) xr[i] = load16(a.res + kk);
+    xg[i] = load16(a.gamma + kk);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // 2. weight reads
+  u32x4 wv[CH][R];
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    const int k = j * 512 + lane * 8;
+    const int kk = k < K ? k : 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) wv[j][r] = load_stream16(wrow[r] + kk);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // 3. x' into LDS: sum of squares per thread, per wave, then over the waves
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int v = threadIdx.x + T * i;
+    const bool ok = v < CH * 64 && 8 * v < K;
+    const half8 xh = as_half8(xa[i]);
+    const half8 rh = IN == kAddNorm ? as_half8(xr[i]) : half8{};
+    half8 co;
+    float part = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float cv = IN == kAddNorm ? (float)rh[e] + (float)xh[e] : (float)xh[e];
+      part += cv * cv;
+      co[e] = (half_t)cv;
+    }
+    ss += ok ? part : 0.f;
+    if (IN == kAddNorm && blockIdx.x == 0 && ok)
+      *reinterpret_cast<u32x4*>(a.res_out + 8 * v) = as_u32x4(co);
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) s_ss[w] = ss;
+  __syncthreads();
+  ss = (s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3]);
+  const float inv = 1.0f / sqrtf(ss / (float)K + a.eps);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int v = threadIdx.x + T * i;
+    if (v < CH * 64) {
+      const half8 xh = as_half8(xa[i]);
+      const half8 rh = IN == kAddNorm ? as_half8(xr[i]) : half8{};
+      const half8 gh = as_half8(xg[i]);
+      half8 xp;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float cv = IN == kAddNorm ? (float)rh[e] + (float)xh[e] : (float)xh[e];
+        xp[e] = (half_t)(cv * inv * (float)gh[e]);
+      }
+      if (8 * v >= K) xp = half8{};
+      *reinterpret_cast<u32x4*>(&s_x[8 * v]) = as_u32x4(xp);
+    }
+  }
+  __syncthreads();
+  // 4. dot products
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.f;
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    const half8 xh = as_half8(*reinterpret_cast<const u32x4*>(&s_x[j * 512 + lane * 8]));
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = dot8(wv[j][r], xh, acc[r]);
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+  const int o0 = gwave * P;
+  if (lane < P && o0 + lane < N) {
+    float g = acc[0], u = acc[R > 1 ? 1 : 0];
+#pragma unroll
+    for (int i = 1; i < P; ++i)
+      if (lane == i) {
+        g = acc[OUT == kSiluPairs ? 2 * i : i];
+        u = acc[OUT == kSiluPairs ? 2 * i + 1 : i];
+      }
+    if (OUT == kSiluPairs)
+      y[o0 + lane] = (half_t)silu_mul1((float)(half_t)g, (float)(half_t)u);
+    else
+      y[o0 + lane] = (half_t)g;
+  }
+}
+
 // CH > 0: exactly CH chunks; CH == 0: any K.  N = output rows.  WAVES waves
 // per workgroup: one for the layer projections (measured 5-10% faster than
 // four on MI355X: finished waves free their CU slot at once), four for the
@@ -529,6 +657,32 @@ static hipError_t launch_gemv_mode(const void* W, const GemvArgs& a, void* y, in
   // Exact-chunk kernels for the Qwen3 decode shapes: hidden 2560 / 4096 /
   // 5120 (5, 8, 10 chunks), attention width 4096 / 8192 (8, 16), MLP width
   // 9728 / 12288 (19, 24).
+  if constexpr (IN != kPlain) {
+    // norm inputs: x' shared through LDS; two rows per wave, two (gate, up)
+    // pairs per wave at 5 chunks (one pair at 8 and 10: register budget)
+    auto lds = [&](auto ch, auto r) {
+      constexpr int CH = decltype(ch)::value, R = decltype(r)::value;
+      constexpr int P = OUT == kSiluPairs ? R / 2 : R;
+      const long waves = (N + P - 1) / P;
+      gemv_norm_lds_kernel<R, IN, OUT, CH>
+          <<<(unsigned)((waves + kNormWaves - 1) / kNormWaves), kNormWaves * 64, 0, stream>>>(
+              (const half_t*)W, a, (half_t*)y, N, K);
+      return hipGetLastError();
+    };
+    using I2 = std::integral_constant<int, 2>;
+    using I4 = std::integral_constant<int, 4>;
+    switch (nchunks) {
+      case 5:
+        if constexpr (OUT == kSiluPairs) return lds(std::integral_constant<int, 5>{}, I4{});
+        else return lds(std::integral_constant<int, 5>{}, I2{});
+      case 8:
+        return lds(std::integral_constant<int, 8>{}, I2{});
+      case 10:
+        return lds(std::integral_constant<int, 10>{}, I2{});
+      default:
+        break;
+    }
+  }
   switch (nchunks) {
     case 5:
       if (two) gemv_launch<2, IN, OUT, 5>(W, a, y, N, K, stream);
@@ -547,11 +701,13 @@ static hipError_t launch_gemv_mode(const void* W, const GemvArgs& a, void* y, in
   // Long K occurs only for plain inputs (attention width, MLP width).
   if constexpr (IN == kPlain && OUT == kRows) {
     switch (nchunks) {
+      // two rows per wave up to 19 chunks (down 2560 x 9728: 9.5 vs 10.3 us
+      // with one row); one at 24, where two would not fit the registers
       case 16:
-        gemv_launch<1, IN, OUT, 16>(W, a, y, N, K, stream);
+        gemv_launch<2, IN, OUT, 16>(W, a, y, N, K, stream);
         return hipGetLastError();
       case 19:
-        gemv_launch<1, IN, OUT, 19>(W, a, y, N, K, stream);
+        gemv_launch<2, IN, OUT, 19>(W, a, y, N, K, stream);
         return hipGetLastError();
       case 24:
         gemv_launch<1, IN, OUT, 24>(W, a, y, N, K, stream);

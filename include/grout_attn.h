@@ -113,7 +113,8 @@ int grout_fmha_prefill(const void* q, const void* k_cache, const void* v_cache, 
 
 /* Split count the library picks for a live context of ctx_len positions
  * (the reference's FMHA_NUM_KV_SPLITS default / per-context overrides,
- * src/model.rs:135-141). */
+ * src/model.rs:135-141): 1 up to 128 positions, else one split per 32
+ * positions, at most ceil(256 / num_kv_heads) (one workgroup per CU). */
 int grout_attn_decode_default_splits(int ctx_len, int num_q_heads, int num_kv_heads);
 
 /* Bytes of fp32 scratch grout_attn_decode needs for num_splits splits:

@@ -98,6 +98,12 @@ def test_decode_split_defaults_and_workspace():
     assert L.grout_attn_decode_default_splits(4096, 32, 8) == 32
     assert L.grout_attn_decode_default_splits(32768, 64, 8) == 32
     assert L.grout_attn_decode_default_splits(100, 32, 8) == 1
+    assert L.grout_attn_decode_default_splits(128, 32, 8) == 1
+    assert L.grout_attn_decode_default_splits(129, 32, 8) == 5
+    assert L.grout_attn_decode_default_splits(512, 32, 8) == 16
+    assert L.grout_attn_decode_default_splits(1024, 32, 8) == 32
+    assert L.grout_attn_decode_default_splits(1024, 64, 4) == 32
+    assert L.grout_attn_decode_default_splits(40960, 32, 1) == 256
     ws = L.grout_attn_decode_workspace_bytes(64, 8, 128, 64)
     assert ws == 8 * 64 * 8 * 130 * 4  # fp32 partial acc + (max, sum) per (kv head, split, head)
     assert L.grout_attn_decode_workspace_bytes(64, 8, 96, 64) == 0
