@@ -17,8 +17,10 @@
 //    loop), rows XOR-swizzled in 16-byte chunks so that both fragment reads
 //    below are bank-conflict free.  Small tiles measured faster than larger
 //    or deeper-buffered ones (32-position tiles, two tiles in flight, or a
-//    4-slot ring filled by direct-to-LDS loads): the memory system streams
-//    best with ~8 KiB per wave outstanding;
+//    4-slot ring filled by direct-to-LDS loads; two tiles in flight again
+//    with the current loop: 23.9 against 22.7 us at 32k, also slower at 8k
+//    and 16k): the memory system streams best with ~8 KiB per wave
+//    outstanding;
 //  * S^T = K.Q^T on v_mfma_f32_16x16x32_f16: A = the tile's 16 K rows, B = Q^T
 //    with the group's query heads as the 16 columns (G <= 16, zero padded);
 //  * O^T = V^T.P^T on v_mfma_f32_16x16x16_f16 (16 positions = its k): the
