@@ -129,6 +129,7 @@ def test_decode_attention_vs_oracle(gpu, Hq, Hkv, ctx, max_ctx, splits):
     (64, 8, 8191, 32768, None),   # 32B, G = 8
     (64, 8, 16383, 32768, None),  # config 4 at ctx 16384
     (32, 2, 100, 160, 3),         # G = 16, ragged
+    (32, 2, 100, 160, 1),         # G = 16, one split: a group also takes row 16
     (40, 8, 16, 64, 1),           # G = 5, the new row opens a tile
     (8, 8, 0, 64, 1),             # first position
     (16, 8, 47, 64, 7),           # more splits than tiles
@@ -161,6 +162,33 @@ def test_fused_decode_step_vs_oracle(gpu, Hq, Hkv, pos, max_ctx, splits):
     assert np.array_equal(host(kc_d), kc_ref)
     assert np.array_equal(host(vc_d), vc_ref)
     assert_close(host_f32(out), ref, f"fused decode Hq={Hq} pos={pos} splits={splits}")
+
+
+@pytest.mark.parametrize("pos,splits", [(64, None), (64, 1), (1000, 3)])
+def test_fused_decode_position_past_cache_writes_nothing(gpu, pos, splits):
+    """A position at or past max_ctx (a graph replayed one step too far) must
+    not write the cache: both caches stay bit-identical, and the output is the
+    attention of the q rows rotated at the last table row over all max_ctx
+    cached positions."""
+    Hq, Hkv, max_ctx = 16, 8, 64
+    _say("fused_decode_past", Hq, Hkv, pos, max_ctx, splits)
+    qkv = normal("pqkv", ((Hq + 2 * Hkv) * D,))
+    gq, gk = gamma("pgq"), gamma("pgk")
+    cos, sin = O.rope_table(max_ctx, D, 1e6)
+    kc = normal("pkc", (Hkv, max_ctx, D))
+    vc = normal("pvc", (Hkv, max_ctx, D))
+    q_ref = O.qk_norm_rope_kv_decode(qkv, gq, gk, cos, sin, kc.copy(), vc.copy(), max_ctx - 1,
+                                     Hq, Hkv, 1e-6)
+    ref = O.attention_decode(q_ref, kc, vc, max_ctx - 1, nthreads=8)
+    rope = gpu.ops.rope_tables(max_ctx)
+    kc_d, vc_d = dev(kc), dev(vc)
+    p = torch.tensor([pos], dtype=torch.int32, device="cuda")
+    out = gpu.ops.attn_decode_fused(dev(qkv), dev(gq), dev(gk), rope, kc_d, vc_d, p, Hq,
+                                    num_splits=splits)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(kc_d), kc)
+    assert np.array_equal(host(vc_d), vc)
+    assert_close(host_f32(out), ref, f"fused decode past the cache pos={pos} splits={splits}")
 
 
 def test_decode_split_then_merge_matches_fused_call(gpu):
