@@ -520,7 +520,7 @@ int check_part(const grout_wpart& p, int k, const char* what, int layer) {
   else
     GROUT_NEED(grout::qweight_bytes(p.fmt, p.rows, k) != 0, GROUT_ENOTSUP,
                "%s%s%d: format %d does not fit k=%d (a multiple of the block size, at most "
-               "16384)",
+               "32768)",
                what, lname, layer, p.fmt, k);
   return GROUT_OK;
 }
@@ -793,7 +793,7 @@ static int check_q(int fmt, int n, int k) {
              GROUT_ENOTSUP, "weight format %d: Q8_0 (8), Q4_K (12), Q5_K (13) or Q6_K (14) expected",
              fmt);
   GROUT_NEED(grout::qweight_bytes(fmt, n, k) != 0, GROUT_EINVAL,
-             "[%d][%d] of format %d: k must be a multiple of the block size and <= 16384", n, k,
+             "[%d][%d] of format %d: k must be a multiple of the block size and <= 32768", n, k,
              fmt);
   return GROUT_OK;
 }

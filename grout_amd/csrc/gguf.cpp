@@ -521,7 +521,7 @@ int plan_parts(Plan& pl, const std::vector<const Tensor*>& mats, const std::vect
     } else {
       bytes = grout::qweight_bytes(p.fmt, p.rows, k);
       GROUT_NEED(bytes != 0, GROUT_ENOTSUP,
-                 "%s: format %d does not fit k=%d (a multiple of the block size, at most 16384)",
+                 "%s: format %d does not fit k=%d (a multiple of the block size, at most 32768)",
                  what.c_str(), p.fmt, k);
       pl.staging = std::max(pl.staging, raw);
     }

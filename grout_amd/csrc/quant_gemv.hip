@@ -28,7 +28,9 @@
 
 namespace grout {
 
-constexpr int kQMaxK = 16384;  // x staged in LDS (at most 32 KiB)
+constexpr int kQMaxK = 32768;  // x staged in LDS (at most 64 KiB): every Qwen3 K up to
+                               // 32B's ffn_down (25600); the 4-row workgroup then needs
+                               // <= 107 KiB of LDS (gfx950: 160 KiB per workgroup)
 
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
@@ -855,9 +857,18 @@ static size_t gemv_q_lds(int R, int S, int K) {
          (size_t)R * (FMT == 8 ? K / 32 : K / 16) * 4 + (size_t)R * S * 4 + 4 * 4;
 }
 
+// Largest LDS allocation one workgroup may make on the current device.
+static size_t qmax_lds() {
+  int dev = 0, v = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+    return 65536;
+  return (size_t)v;
+}
+
 template <int FMT, bool NORM>
-static void gemv_q_launch(const void* W, const void* x, void* y, int N, int K, bool silu,
-                          const QNorm& nz, hipStream_t stream) {
+static hipError_t gemv_q_launch(const void* W, const void* x, void* y, int N, int K, bool silu,
+                                const QNorm& nz, hipStream_t stream) {
   const int rows = silu ? 2 * N : N;
   const QLayout L = qlayout(FMT, (size_t)rows, (size_t)K);
   const int np = K % 512 == 0 ? K / 512 : 0;  // pieces per lane of a whole row
@@ -868,15 +879,16 @@ static void gemv_q_launch(const void* W, const void* x, void* y, int N, int K, b
     const int npw = npw_tall(np) ? np : 0;
     if (silu) gemv_q_go<FMT, true, 16, 1, NORM>(npw, grid, gemv_q_lds<FMT>(16, 1, K), W, x, y, N, K, L, nz, stream);
     else gemv_q_go<FMT, false, 16, 1, NORM>(npw, grid, gemv_q_lds<FMT>(16, 1, K), W, x, y, N, K, L, nz, stream);
-    return;
+    return hipGetLastError();
   }
   // short: 4 rows per workgroup, each row split over S waves so that the grid
   // holds about 2048 waves or more
   const int per = silu ? 2 : 4;
+  if (gemv_q_lds<FMT>(4, 4, K) > qmax_lds()) return hipErrorInvalidValue;
   const unsigned grid = (unsigned)((N + per - 1) / per);
   if (silu) {
     gemv_q_go<FMT, true, 4, 0, NORM>(0, grid, gemv_q_lds<FMT>(4, 1, K), W, x, y, N, K, L, nz, stream);
-    return;
+    return hipGetLastError();
   }
   int S = 0, npw = 0;
   if (np > 0) {
@@ -889,6 +901,7 @@ static void gemv_q_launch(const void* W, const void* x, void* y, int N, int K, b
   else if (S == 1) gemv_q_go<FMT, false, 4, 1, NORM>(npw, grid, gemv_q_lds<FMT>(4, 1, K), W, x, y, N, K, L, nz, stream);
   else if (S == 2) gemv_q_go<FMT, false, 4, 2, NORM>(npw, grid, gemv_q_lds<FMT>(4, 2, K), W, x, y, N, K, L, nz, stream);
   else gemv_q_go<FMT, false, 4, 4, NORM>(npw, grid, gemv_q_lds<FMT>(4, 4, K), W, x, y, N, K, L, nz, stream);
+  return hipGetLastError();
 }
 
 hipError_t launch_gemv_q(int fmt, const void* W, const void* x, void* y, int N, int K, bool silu,
@@ -904,23 +917,18 @@ hipError_t launch_gemv_q_norm(int fmt, const void* W, const void* residual, cons
   const bool norm = gamma != nullptr;
   switch (fmt) {
     case 8:
-      if (norm) gemv_q_launch<8, true>(W, x, y, N, K, silu, nz, stream);
-      else gemv_q_launch<8, false>(W, x, y, N, K, silu, nz, stream);
-      break;
+      return norm ? gemv_q_launch<8, true>(W, x, y, N, K, silu, nz, stream)
+                  : gemv_q_launch<8, false>(W, x, y, N, K, silu, nz, stream);
     case 12:
-      if (norm) gemv_q_launch<12, true>(W, x, y, N, K, silu, nz, stream);
-      else gemv_q_launch<12, false>(W, x, y, N, K, silu, nz, stream);
-      break;
+      return norm ? gemv_q_launch<12, true>(W, x, y, N, K, silu, nz, stream)
+                  : gemv_q_launch<12, false>(W, x, y, N, K, silu, nz, stream);
     case 13:
-      if (norm) gemv_q_launch<13, true>(W, x, y, N, K, silu, nz, stream);
-      else gemv_q_launch<13, false>(W, x, y, N, K, silu, nz, stream);
-      break;
+      return norm ? gemv_q_launch<13, true>(W, x, y, N, K, silu, nz, stream)
+                  : gemv_q_launch<13, false>(W, x, y, N, K, silu, nz, stream);
     default:
-      if (norm) gemv_q_launch<14, true>(W, x, y, N, K, silu, nz, stream);
-      else gemv_q_launch<14, false>(W, x, y, N, K, silu, nz, stream);
-      break;
+      return norm ? gemv_q_launch<14, true>(W, x, y, N, K, silu, nz, stream)
+                  : gemv_q_launch<14, false>(W, x, y, N, K, silu, nz, stream);
   }
-  return hipGetLastError();
 }
 
 hipError_t launch_qgather(int fmt, const void* W, int N, int K, const uint32_t* ids, int rows,

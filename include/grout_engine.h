@@ -130,7 +130,7 @@ int grout_gemv_rms_norm_silu_mul(const void* W, const void* residual, const void
 
 /* Device bytes of an [n][k] matrix of format fmt in the GEMV layout (0 when
  * the format or shape is unsupported: k a multiple of the block size, 32 for
- * Q8_0 and 256 for the K-quants, at most 16384). */
+ * Q8_0 and 256 for the K-quants, at most 32768). */
 size_t grout_qweight_bytes(int fmt, int n, int k);
 
 /* Splits n rows of ggml blocks (device memory, rows contiguous) into the GEMV

@@ -40,6 +40,7 @@
  * weights, accumulated in fp64 here (the reference accumulates in fp32), so
  * the GPU result differs from this only by fp32 rounding.
  */
+#include <stdlib.h>
 #include <stddef.h>
 #include <stdint.h>
 #include <string.h>
@@ -158,9 +159,9 @@ int go_dequant_decode(int fmt, const uint8_t* blocks, size_t n, float* out) {
  * of K weights stored as ggml blocks, rows contiguous. */
 int go_gemv_q(int fmt, const uint8_t* blocks, int N, int K, const uint16_t* x, double* y) {
   const int be = go_qblock_elems(fmt), bb = go_qblock_bytes(fmt);
-  if (bb < 0 || K % be) return -1;
-  float row[16384];
-  if (K > 16384) return -1;
+  if (bb < 0 || K <= 0 || K % be) return -1;
+  float* row = (float*)malloc((size_t)K * sizeof(float));
+  if (!row) return -2;
   const size_t row_bytes = (size_t)(K / be) * (size_t)bb;
   for (int r = 0; r < N; ++r) {
     dequant_mode(fmt, blocks + (size_t)r * row_bytes, (size_t)K, row, 1);
@@ -168,5 +169,6 @@ int go_gemv_q(int fmt, const uint8_t* blocks, int N, int K, const uint16_t* x, d
     for (int k = 0; k < K; ++k) s += (double)row[k] * (double)go_h2f(x[k]);
     y[r] = s;
   }
+  free(row);
   return 0;
 }

@@ -186,3 +186,13 @@ def test_gemv_norm_rejects_residual_aliasing_without_gpu():
         assert "alias" in _lib.last_error()
         assert f(p, a, b, p, b, p, 16, 64, 1e-6, None) == -1  # residual_out == x
         assert "alias" in _lib.last_error()
+
+
+def test_low_bit_k_limit_covers_qwen3_without_gpu():
+    """The low-bit GEMVs stage x in LDS: every Qwen3 ffn_down width up to
+    32B's 25600 is accepted, K past 32768 is refused (host-side sizing)."""
+    L = grout_amd.lib()
+    for fmt, blk in ((8, 32), (12, 256), (13, 256), (14, 256)):
+        for k in (17408, 25600, 32768):
+            assert L.grout_qweight_bytes(fmt, 5120, k) > 0, (fmt, k)
+        assert L.grout_qweight_bytes(fmt, 5120, 32768 + blk) == 0, fmt

@@ -74,9 +74,12 @@ FMTS = [(O.Q8_0, "Q8_0"), (O.Q4_K, "Q4_K"), (O.Q5_K, "Q5_K"), (O.Q6_K, "Q6_K")]
 
 @pytest.mark.parametrize("fmt,name", FMTS)
 # 4-row workgroups with 5 / 19 / 8 pieces per lane and the any-K path; 16-row
-# workgroups (>= 16384 rows) with a ragged last workgroup, exact and any-K
+# workgroups (>= 16384 rows) with a ragged last workgroup, exact and any-K;
+# the ffn_down widths of Qwen3-14B (17408, any-K path) and Qwen3-32B (25600,
+# 13 pieces per lane in 4 slices) and the largest K (32768, x in 64 KiB of LDS)
 @pytest.mark.parametrize("n,k", [(6144, 2560), (2560, 9728), (2560, 4096), (37, 256), (1, 512),
-                                 (16400, 2560), (16391, 768)])
+                                 (16400, 2560), (16391, 768), (300, 17408), (300, 25600),
+                                 (7, 32768)])
 def test_gemv_q_vs_oracle(gpu, fmt, name, n, k):
     L = gpu.lib()
     print(f"gemv_q {name} n={n} k={k}", flush=True)
@@ -172,6 +175,8 @@ def test_quant_argument_errors(gpu):
 
     L = gpu.lib()
     assert L.grout_qweight_bytes(O.Q4_K, 10, 300) == 0   # k not a multiple of 256
+    assert L.grout_qweight_bytes(O.Q4_K, 10, 32768) > 0
+    assert L.grout_qweight_bytes(O.Q4_K, 10, 32768 + 256) == 0  # x no longer fits in LDS
     assert L.grout_qweight_bytes(3, 10, 256) == 0         # not a supported format
     buf = torch.empty(1 << 16, dtype=torch.uint8, device="cuda")
     with pytest.raises(GroutError, match="multiple of the block size"):
