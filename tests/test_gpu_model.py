@@ -115,7 +115,11 @@ def test_gemv(gpu, n, k):
 
 
 @pytest.mark.parametrize("mode", ["norm", "add_norm"])
-@pytest.mark.parametrize("n,k", [(6144, 2560), (19456, 2560), (100, 8192), (3, 64)])
+# 5 / 8 / 10-chunk K take the LDS-shared-input kernel (2 rows per wave, 4
+# waves per workgroup): exact and ragged K, ragged N; other K the loop path
+@pytest.mark.parametrize("n,k", [(6144, 2560), (19456, 2560), (100, 8192), (3, 64),
+                                 (37, 2560), (6145, 2304), (1000, 4096), (77, 4000),
+                                 (5, 5120)])
 def test_gemv_rms_norm_fused(gpu, mode, n, k):
     """Norm fused into the GEMV vs the oracle's norm then product.  The fused
     input rounds like the separate kernel; its 1/rms may differ in the last
@@ -151,7 +155,10 @@ def test_gemv_rms_norm_fused(gpu, mode, n, k):
 
 
 @pytest.mark.parametrize("mode", ["norm", "add_norm"])
-@pytest.mark.parametrize("inter,k", [(9728, 2560), (64, 8), (5, 4104), (300, 5120)])
+# two (gate, up) pairs per wave at 5 chunks (odd inter leaves a lone pair),
+# one pair at 8 and 10 chunks
+@pytest.mark.parametrize("inter,k", [(9728, 2560), (64, 8), (5, 4104), (300, 5120),
+                                     (4097, 2560), (9, 2304), (1000, 4096)])
 def test_gemv_rms_norm_silu_mul_fused(gpu, mode, inter, k):
     """gate_up GEMV with the norm input and SiLU * up epilogue vs the oracle's
     norm -> product -> silu_mul.  Tolerance: the gate/up products may differ
