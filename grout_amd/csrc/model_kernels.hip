@@ -373,7 +373,7 @@ __device__ __forceinline__ void gemv_loop(const half_t* __restrict__ W, const Ge
 // wave; kSiluPairs: R / 2 (gate, up) pairs.  Measured on MI355X at the
 // Qwen3-4B shapes (HIP events, rotating weights): QKV 6144 x 2560 6.95 vs
 // 7.83 us, gate_up 19456 x 2560 16.4 vs 20.9 us.
-constexpr int kNormWaves = 4;
+constexpr int kNormWaves = 4;  // the wave sums below add exactly four partials
 
 template <int R, int IN, int OUT, int CH>
 __global__ __launch_bounds__(kNormWaves * 64) void gemv_norm_lds_kernel(
@@ -442,6 +442,7 @@ __global__ __launch_bounds__(kNormWaves * 64) void gemv_norm_lds_kernel(
   ss = wave_sum(ss);
   if (lane == 0) s_ss[w] = ss;
   __syncthreads();
+  static_assert(kNormWaves == 4, "fixed summation order of the wave partials");
   ss = (s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3]);
   const float inv = 1.0f / sqrtf(ss / (float)K + a.eps);
 #pragma unroll

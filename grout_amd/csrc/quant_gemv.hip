@@ -26,6 +26,8 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+#include <atomic>
+
 namespace grout {
 
 constexpr int kQMaxK = 32768;  // x staged in LDS (at most 64 KiB): every Qwen3 K up to
@@ -857,12 +859,22 @@ static size_t gemv_q_lds(int R, int S, int K) {
          (size_t)R * (FMT == 8 ? K / 32 : K / 16) * 4 + (size_t)R * S * 4 + 4 * 4;
 }
 
-// Largest LDS allocation one workgroup may make on the current device.
+// Largest LDS allocation one workgroup may make on the current device
+// (queried once per device; 64 KiB if the query fails).
 static size_t qmax_lds() {
-  int dev = 0, v = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+  constexpr int kDevs = 64;
+  static std::atomic<int> cached[kDevs];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 65536;
+  if (dev >= 0 && dev < kDevs) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) return (size_t)c;
+  }
+  int v = 0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
+      v <= 0)
     return 65536;
+  if (dev >= 0 && dev < kDevs) cached[dev].store(v, std::memory_order_relaxed);
   return (size_t)v;
 }
 
