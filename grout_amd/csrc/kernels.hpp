@@ -6,12 +6,15 @@
 
 namespace grout {
 
+// ldq / ldkv: elements from one token's q (k, v) rows to the next; 0 = packed
+// (Hq * 128, Hkv * 128), e.g. Hq*128 + 2*Hkv*128 for rows of a fused QKV output.
 hipError_t launch_qk_norm_rope_kv_prefill(const void* q, const void* k, const void* v,
                                           const void* gamma_q, const void* gamma_k,
                                           const float* rope_cos, const float* rope_sin,
                                           void* q_out, void* k_cache, void* v_cache, int pos0,
                                           int seq_len, int Hq, int Hkv, long head_stride,
-                                          int max_ctx, float eps, hipStream_t stream);
+                                          int max_ctx, float eps, hipStream_t stream,
+                                          long ldq = 0, long ldkv = 0);
 
 hipError_t launch_qk_norm_rope_kv_decode(const void* qkv, const void* gamma_q,
                                          const void* gamma_k, const float* rope_cos,

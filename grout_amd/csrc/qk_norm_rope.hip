@@ -110,7 +110,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv_prefill8_kernel(
     const half_t* __restrict__ gamma_q, const half_t* __restrict__ gamma_k,
     const float* __restrict__ rope_cos, const float* __restrict__ rope_sin,
     half_t* __restrict__ q_out, half_t* __restrict__ k_cache, half_t* __restrict__ v_cache,
-    int pos0, int rows, int Hq, int Hkv, long head_stride, float eps) {
+    int pos0, int rows, int Hq, int Hkv, long head_stride, float eps, long ldq, long ldkv) {
   const int r = (int)blockIdx.x * 32 + (int)(threadIdx.x >> 3);
   if (r >= rows) return;  // uniform across the 8 lanes of a row group
   const int i = threadIdx.x & 7;
@@ -120,7 +120,9 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv_prefill8_kernel(
   const bool is_q = h < Hq;
   const int kvh = h - Hq;
   // all loads first
-  const half_t* x = is_q ? q + ((size_t)s * Hq + h) * kHeadDim : k + ((size_t)s * Hkv + kvh) * kHeadDim;
+  // token s's rows start ldq (q) / ldkv (k, v) elements apart
+  const half_t* x = is_q ? q + (size_t)s * ldq + (size_t)h * kHeadDim
+                         : k + (size_t)s * ldkv + (size_t)kvh * kHeadDim;
   const u32x4 xlo = load16(x + 8 * i), xhi = load16(x + 64 + 8 * i);
   const half_t* gm = is_q ? gamma_q : gamma_k;
   const half8 glo = as_half8(load16(gm + 8 * i)), ghi = as_half8(load16(gm + 64 + 8 * i));
@@ -132,7 +134,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv_prefill8_kernel(
   const floatx4 s1 = *reinterpret_cast<const floatx4*>(srow + 4);
   u32x4 vlo = {0u, 0u, 0u, 0u}, vhi = {0u, 0u, 0u, 0u};
   if (!is_q) {
-    const half_t* vr = v + ((size_t)s * Hkv + kvh) * kHeadDim;
+    const half_t* vr = v + (size_t)s * ldkv + (size_t)kvh * kHeadDim;
     vlo = load16(vr + 8 * i);
     vhi = load16(vr + 64 + 8 * i);
   }
@@ -158,16 +160,21 @@ hipError_t launch_qk_norm_rope_kv_prefill(const void* q, const void* k, const vo
                                           const float* rope_cos, const float* rope_sin,
                                           void* q_out, void* k_cache, void* v_cache, int pos0,
                                           int seq_len, int Hq, int Hkv, long head_stride,
-                                          int max_ctx, float eps, hipStream_t stream) {
+                                          int max_ctx, float eps, hipStream_t stream, long ldq,
+                                          long ldkv) {
   (void)max_ctx;  // the caller checked pos0 + seq_len <= max_ctx
   const long rows = (long)seq_len * (Hq + Hkv);
   if (rows <= 0 || rows > 0x7fffffffL) return hipErrorInvalidValue;
+  if (ldq == 0) ldq = (long)Hq * kHeadDim;
+  if (ldkv == 0) ldkv = (long)Hkv * kHeadDim;
+  if (ldq < (long)Hq * kHeadDim || ldkv < (long)Hkv * kHeadDim || ldq % 8 || ldkv % 8)
+    return hipErrorInvalidValue;
   // 32 rows per 256-thread workgroup measured fastest on MI355X (S=2048, 4B:
   // 8.6-8.7 us; 64/128/512 threads 8.9-9.5 us; two rows per lane group 9.8-10.9 us)
   qk_norm_rope_kv_prefill8_kernel<<<(unsigned)((rows + 31) / 32), 256, 0, stream>>>(
       (const half_t*)q, (const half_t*)k, (const half_t*)v, (const half_t*)gamma_q,
       (const half_t*)gamma_k, rope_cos, rope_sin, (half_t*)q_out, (half_t*)k_cache,
-      (half_t*)v_cache, pos0, (int)rows, Hq, Hkv, head_stride, eps);
+      (half_t*)v_cache, pos0, (int)rows, Hq, Hkv, head_stride, eps, ldq, ldkv);
   return hipGetLastError();
 }
 
