@@ -294,18 +294,7 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES <= 4 ? 2 : 1)) void attn_decode_
     }
   };
 
-  // The loads of tile k+1 are issued before tile k is stored (two register
-  // copies), so they overlap the store as well as the compute.
-  if (!FUSED && nmine > 0) load_tile(0);  // FUSED: issued in the prologue
-  for (int k = 0; k < nmine; ++k) {
-    u32x4 ck[4], cv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      ck[i] = rk[i];
-      cv[i] = rv[i];
-    }
-    if (k + 1 < nmine) load_tile(k + 1);
-    store_tile(ck, cv);  // after this wave's reads of the previous tile (LDS is in order)
+  auto patch_new_row = [&](int k) __attribute__((always_inline)) {
     if (FUSED && owner && tile_of(k) * kTile == t_new) {
       // rows pos .. t_new+15 of the slot get the new K / V row (the loads
       // read the cache's old row pos for all of them)
@@ -318,7 +307,43 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES <= 4 ? 2 : 1)) void attn_decode_
                                     ((chunk ^ dswz(r)) << 4)) = v16;
       }
     }
-    compute(k, &s_buf[0][0]);
+  };
+  if (!FUSED && nmine > 0) load_tile(0);  // FUSED: issued in the prologue
+  if (nmine == 2) {
+    // A wave with two tiles (4k positions over 32 splits) has both in flight
+    // at once: no extra loads, 0.3-0.5 us less per launch than the loop.
+    u32x4 k1[4], v1[4];
+    {
+      const int t = tile_of(1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = min(t * kTile + 4 * i + kb, s_kv - 1);
+        const unsigned off = (unsigned)row * 256u + (unsigned)col * 16u;
+        k1[i] = load_stream16(kh + off);
+        v1[i] = load_stream16(vh + off);
+      }
+    }
+    store_tile(rk, rv);
+    patch_new_row(0);
+    compute(0, &s_buf[0][0]);
+    store_tile(k1, v1);  // after this wave's reads of tile 0 (LDS is in order)
+    patch_new_row(1);
+    compute(1, &s_buf[0][0]);
+  } else {
+    // The loads of tile k+1 are issued before tile k is stored (two register
+    // copies), so they overlap the store as well as the compute.
+    for (int k = 0; k < nmine; ++k) {
+      u32x4 ck[4], cv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ck[i] = rk[i];
+        cv[i] = rv[i];
+      }
+      if (k + 1 < nmine) load_tile(k + 1);
+      store_tile(ck, cv);  // after this wave's reads of the previous tile (LDS is in order)
+      patch_new_row(k);
+      compute(k, &s_buf[0][0]);
+    }
   }
   __syncthreads();  // all waves are done with their tile buffers before they are reused
 
