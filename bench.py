@@ -23,7 +23,7 @@ import time
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 # HBM bytes per split-kernel launch (Qwen3-32B, ctx 32768) by split count, measured with
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by a plain-copy calibration (x2.0, x1.0).
-DECODE32B_TRAFFIC_BYTES = {32: 134.31e6 + 1.065e6}
+DECODE32B_TRAFFIC_BYTES = {32: 134.32e6 + 1.065e6}
 DECODE32B_TRAFFIC_SOURCE = "profiles/attn_decode_split_qwen3-32b_ctx_sweep.md"
 F16_MFMA_PEAK_TFLOPS = 2516.6  # MI355X dense fp16 MFMA, TFLOP/s
 D = 128
