@@ -224,7 +224,37 @@ def bench_prefill(ops, S, Hq, Hkv, steps, warmup):
     ms = time_launches(lambda i=0: ops.fmha_prefill(q, kc, vc, 0, out=out), steps, warmup,
                        torch.cuda.current_stream(dev))
     flop = 4.0 * Hq * D * S * (S + 1) / 2
-    return dict(ms=ms, flop=flop)
+    return dict(ms=ms, flop=flop, library=bench_prefill_library(q, kc, vc, out, steps, warmup))
+
+
+def bench_prefill_library(q, kc, vc, out, steps, warmup):
+    """PyTorch's fused causal attention on the same inputs, as a vendor-library
+    point of comparison: F.scaled_dot_product_attention restricted to its flash
+    backend (on ROCm an AOTriton kernel), fp16, is_causal, K/V expanded to one
+    copy per query head (the flash backend takes equal head counts).  Reported
+    with the largest |difference| from this build's output."""
+    import torch
+    import torch.nn.functional as F
+
+    try:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+
+        S, Hq, _ = q.shape
+        G = Hq // kc.shape[0]
+        qt = q.permute(1, 0, 2).unsqueeze(0).contiguous()
+        kt = kc[:, :S].repeat_interleave(G, 0).unsqueeze(0).contiguous()
+        vt = vc[:, :S].repeat_interleave(G, 0).unsqueeze(0).contiguous()
+        call = lambda i=0: F.scaled_dot_product_attention(qt, kt, vt, is_causal=True,
+                                                          scale=D ** -0.5)
+        with sdpa_kernel(SDPBackend.FLASH_ATTENTION):
+            ref = call()
+            ms = time_launches(call, steps, warmup, torch.cuda.current_stream(q.device), graph=False)
+        diff = (ref[0].permute(1, 0, 2).float() - out.float()).abs().max().item()
+        del qt, kt, vt, ref
+        return dict(name="torch sdpa flash (AOTriton), K/V expanded to Hq heads", ms=ms,
+                    max_abs_diff=diff)
+    except Exception as e:  # noqa: BLE001 - reported, not fatal: a comparison only
+        return dict(name="torch sdpa flash", error=f"{type(e).__name__}: {str(e)[:160]}")
 
 
 def bench_norm(ops, S, Hq, Hkv, max_ctx, steps, warmup):
@@ -667,6 +697,14 @@ def main():
             t = rr["flop"] / (rr["ms"] * 1e-3) / 1e12
             sweep[str(S)] = {"us": round(rr["ms"] * 1e3, 2), "tflops": round(t, 1),
                              "mfma_frac": round(t / F16_MFMA_PEAK_TFLOPS, 4), "flop": rr["flop"]}
+            lib = rr.get("library") or {}
+            if "ms" in lib:
+                lt = rr["flop"] / (lib["ms"] * 1e-3) / 1e12
+                sweep[str(S)]["library"] = {"name": lib["name"], "us": round(lib["ms"] * 1e3, 2),
+                                            "tflops": round(lt, 1),
+                                            "max_abs_diff": round(lib["max_abs_diff"], 6)}
+            elif lib:
+                sweep[str(S)]["library"] = lib
         line["prefill_sweep"] = sweep
     if "decode4b" in res:
         r = res["decode4b"]
