@@ -22,8 +22,9 @@
 //  * causal balance: workgroup r owns the complementary q blocks h = nqb-1-r
 //    and l = r (their tile counts add up to a constant).  Team A takes tiles
 //    [0, a) of h, team B all tiles of l and then tiles [a, T_h) of h, with
-//    a = ceil((T_h + T_l) / 2); B's partial (m, l, acc) of h is merged into
-//    A's through LDS at the end.  With too few pairs to fill the GPU each
+//    a = ceil((T_h + T_l) / 2); the two partials (m, l, acc) of h meet in
+//    LDS at the end and each team finishes half of h's d range.  With too
+//    few pairs to fill the GPU each
 //    workgroup takes a single q block (T_l = 0), heaviest first;
 //  * K and V tiles (64 positions, 16 KiB each) go straight from the cache into
 //    double-buffered, XOR-swizzled LDS slots with buffer_load ... lds.  A
@@ -444,14 +445,20 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
     wait_vm_keep8();
   };
 
-  auto write_rows = [&](int qb, const float (&lrow)[2]) __attribute__((always_inline)) {
+  const std::integral_constant<int, 0> c0;
+  const std::integral_constant<int, 4> c4;
+  const std::integral_constant<int, 8> c8;
+  // Output rows of block qb, d blocks [DB0, DB0 + NDB).
+  auto write_rows = [&](auto db0_c, auto ndb_c, int qb, const float (&lrow)[2])
+                        __attribute__((always_inline)) {
+    constexpr int DB0 = decltype(db0_c)::value, NDB = decltype(ndb_c)::value;
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
       if (!row_valid(qb, mb)) continue;
       const float inv = 1.0f / lrow[mb];
       half_t* orow = out + ((size_t)(qb * BQ + rpos(mb)) * Hq + rhead(mb)) * kHeadDim;
 #pragma unroll
-      for (int db = 0; db < 8; ++db) {
+      for (int db = DB0; db < DB0 + NDB; ++db) {
         half4 o;
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[i] = (half_t)(acc[mb][db][i] * inv);
@@ -474,7 +481,7 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
     if (j + 1 == n0 && n1 > 0) {
       float lrow[2];
       row_sums(lrow);
-      write_rows(qb0, lrow);
+      write_rows(c0, c8, qb0, lrow);
       reset_state();
     }
   };
@@ -527,38 +534,59 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
   float lrow[2];
   row_sums(lrow);
   if (!merge_h) {
-    if (n > 0) write_rows(n1 > 0 ? qb1 : qb0, lrow);
+    if (n > 0) write_rows(c0, c8, n1 > 0 ? qb1 : qb0, lrow);
     return;
   }
-  // Team B holds tiles [a, T_h) of block h: its (m, l, acc) go through LDS
-  // (team 1's slots take acc, team 0's first K slot takes m and l) and team A
-  // combines them with its own tiles [0, a).  Same wave index, same lane:
-  // same rows and columns.
+  // Team B holds tiles [a, T_h) of block h, team A tiles [0, a): same wave
+  // index, same lane, same rows and columns.  Each team finishes half of the
+  // d blocks (A 0-3, B 4-7): it publishes the other half of its (acc) and its
+  // (m, l) through LDS (slot arrays of the wave index: A's half in the first
+  // 8 KiB, B's in the second; team t's (m, l) in team 0's first K slot at
+  // t * 4 KiB), then combines its own half with the other team's, A's terms
+  // first in both teams.
   unsigned char* const accbuf = w == 0 ? s_k0[1] : w == 1 ? s_k1[1] : w == 2 ? s_v0[1] : s_v1[1];
   float* const mlbuf = reinterpret_cast<float*>(s_k0[0] + w * 1024) + lane * 4;
-  if (team == 1) {
+  const int other = 1 - team;
+  auto xchg = [&](auto give_c) __attribute__((always_inline)) {
+    constexpr int GIVE = decltype(give_c)::value;
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-      for (int db = 0; db < 8; ++db)
-        *reinterpret_cast<floatx4*>(accbuf + ((mb * 8 + db) * 64 + lane) * 16) = acc[mb][db];
-    *reinterpret_cast<floatx4*>(mlbuf) = floatx4{m[0], m[1], lrow[0], lrow[1]};
-  }
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<floatx4*>(accbuf + team * 8192 + ((mb * 4 + i) * 64 + lane) * 16) =
+            acc[mb][GIVE + i];
+  };
+  if (team == 0)
+    xchg(c4);
+  else
+    xchg(c0);
+  *reinterpret_cast<floatx4*>(mlbuf + team * 1024) = floatx4{m[0], m[1], lrow[0], lrow[1]};
   lds_barrier();
-  if (team == 0) {
-    const floatx4 mlb = *reinterpret_cast<const floatx4*>(mlbuf);
+  const floatx4 mlo = *reinterpret_cast<const floatx4*>(mlbuf + other * 1024);
+  auto finish = [&](auto keep_c) __attribute__((always_inline)) {
+    constexpr int KEEP = decltype(keep_c)::value;
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
-      const float mn = fmaxf(m[mb], mlb[mb]);
-      const float sa = fast_exp2(m[mb] - mn), sb = fast_exp2(mlb[mb] - mn);
-      lrow[mb] = lrow[mb] * sa + mlb[2 + mb] * sb;
+      const float ma = team == 0 ? m[mb] : mlo[mb], mbb = team == 0 ? mlo[mb] : m[mb];
+      const float la = team == 0 ? lrow[mb] : mlo[2 + mb], lb = team == 0 ? mlo[2 + mb] : lrow[mb];
+      const float mn = fmaxf(ma, mbb);
+      const float sa = fast_exp2(ma - mn), sb = fast_exp2(mbb - mn);
+      const float ss = team == 0 ? sa : sb, so = team == 0 ? sb : sa;
+      lrow[mb] = la * sa + lb * sb;
 #pragma unroll
-      for (int db = 0; db < 8; ++db)
-        acc[mb][db] = acc[mb][db] * sa +
-                      *reinterpret_cast<const floatx4*>(accbuf + ((mb * 8 + db) * 64 + lane) * 16) * sb;
+      for (int i = 0; i < 4; ++i) {
+        const floatx4 mine = acc[mb][KEEP + i] * ss;
+        const floatx4 theirs = *reinterpret_cast<const floatx4*>(
+                                   accbuf + other * 8192 + ((mb * 4 + i) * 64 + lane) * 16) * so;
+        acc[mb][KEEP + i] = team == 0 ? mine + theirs : theirs + mine;
+      }
     }
-    write_rows(h, lrow);
-  }
+    write_rows(keep_c, c4, h, lrow);
+  };
+  if (team == 0)
+    finish(c0);
+  else
+    finish(c4);
 }
 
 // GROUT_FMHA_PREFILL_PAIRED=0/1 forces the single-block / paired work split
