@@ -138,17 +138,26 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES <= 4 ? 2 : 1)) void attn_decode_
   // logical chunk l%16, of K (rk[i]) and of V (rv[i]); it is stored at chunk
   // (l%16) ^ dswz(row) of the wave's LDS tile.
   u32x4 rk[4], rv[4];
-  auto load_tile = [&](int k) __attribute__((always_inline)) {
-    const int t = tile_of(k);
+  // The tile's four K loads go out before its four V loads (and K is stored
+  // to LDS first): each wave streams one tensor at a time, which HBM serves
+  // faster than alternating K and V requests, and the K stores need not wait
+  // for V.  Qwen3-32B split + merge step, same box: 24.29 -> 23.89 us at 32k,
+  // 14.78 -> 14.42 at 16k, 10.52 -> 9.97 at 8k (bit-identical output).
+  auto load_kv = [&](int t, u32x4 (&tk)[4], u32x4 (&tv)[4]) __attribute__((always_inline)) {
+    unsigned off[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       // rows past the context are masked; read a live row instead
       const int row = min(t * kTile + 4 * i + kb, s_kv - 1);
-      const unsigned off = (unsigned)row * 256u + (unsigned)col * 16u;
-      rk[i] = load_stream16(kh + off);
-      rv[i] = load_stream16(vh + off);
+      off[i] = (unsigned)row * 256u + (unsigned)col * 16u;
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) tk[i] = load_stream16(kh + off[i]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) tv[i] = load_stream16(vh + off[i]);
   };
+  auto load_tile = [&](int k) __attribute__((always_inline)) { load_kv(tile_of(k), rk, rv); };
   // FUSED prologue: 32-lane group gi of the workgroup normalizes and rotates
   // rows gi, gi + 2 WAVES, ...: rows 0..G-1 are the group's q heads, row G
   // (owner only) the new K row; the owner also stages the V row.  The reads
@@ -230,10 +239,9 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES <= 4 ? 2 : 1)) void attn_decode_
   for (int i = 0; i < 4; ++i) st_off[i] = wave_off + (4 * i + kb) * 256 + ((col ^ dswz(4 * i + kb)) << 4);
   auto store_tile = [&](const u32x4 (&tk)[4], const u32x4 (&tv)[4]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<u32x4*>(&s_buf[0][0] + st_off[i]) = tk[i];
-      *reinterpret_cast<u32x4*>(&s_buf[0][0] + st_off[i] + 4096) = tv[i];
-    }
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(&s_buf[0][0] + st_off[i]) = tk[i];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(&s_buf[0][0] + st_off[i] + 4096) = tv[i];
   };
   // Fragment offsets (this wave's slot base included):
   //  K (A of S^T): row col, logical chunk 4c + kb;
@@ -315,16 +323,7 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES <= 4 ? 2 : 1)) void attn_decode_
     // A wave with two tiles (4k positions over 32 splits) has both in flight
     // at once: no extra loads, 0.3-0.5 us less per launch than the loop.
     u32x4 k1[4], v1[4];
-    {
-      const int t = tile_of(1);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = min(t * kTile + 4 * i + kb, s_kv - 1);
-        const unsigned off = (unsigned)row * 256u + (unsigned)col * 16u;
-        k1[i] = load_stream16(kh + off);
-        v1[i] = load_stream16(vh + off);
-      }
-    }
+    load_kv(tile_of(1), k1, v1);
     store_tile(rk, rv);
     patch_new_row(0);
     compute(0, &s_buf[0][0]);
