@@ -94,8 +94,13 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES <= 4 ? 2 : 1)) void attn_decode_
   // Wave w's tile buffer is s_buf[w].
   __shared__ __attribute__((aligned(1024))) unsigned char s_buf[WAVES][kSlotBytes];
   __shared__ float s_ml[WAVES][16][2];
-  // the waves' O^T accumulators for the cross-wave merge: [wave][d block][lane]
-  __shared__ floatx4 s_acc[WAVES][8][64];
+  // The waves' O^T accumulators for the cross-wave merge ([d block][lane],
+  // 8 KiB) go into each wave's own tile buffer once its loop is done, so the
+  // workgroup needs 33 KiB (one-split variant: 71 KiB) instead of 66 (137).
+  // Measured the same as a separate array at 66 KiB; the footprint matters
+  // above that: the split pass padded to 99 KiB ran 0.5 us slower per 32k
+  // step, although one workgroup per CU runs either way.
+  static_assert(8 * 64 * sizeof(floatx4) == kSlotBytes, "accumulators fill one tile buffer");
   // FUSED: rotated q rows of the group, then the new K and V rows.
   __shared__ __attribute__((aligned(16))) half_t s_qkv[FUSED ? 18 : 1][kHeadDim];
 
@@ -361,7 +366,7 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES <= 4 ? 2 : 1)) void attn_decode_
     s_ml[w][col][1] = l;
   }
 #pragma unroll
-  for (int db = 0; db < 8; ++db) s_acc[w][db][lane] = acc[db];
+  for (int db = 0; db < 8; ++db) reinterpret_cast<floatx4*>(s_buf[w])[db * 64 + lane] = acc[db];
   __syncthreads();
 
   float M = s_ml[0][col][0];
@@ -380,7 +385,7 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES <= 4 ? 2 : 1)) void attn_decode_
     floatx4 O = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ww = 0; ww < WAVES; ++ww) {
-      const floatx4 a4 = s_acc[ww][db][lane];
+      const floatx4 a4 = reinterpret_cast<const floatx4*>(s_buf[ww])[db * 64 + lane];
 #pragma unroll
       for (int i = 0; i < 4; ++i) O[i] += wgt[ww] * a4[i];
     }
