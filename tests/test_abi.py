@@ -38,6 +38,56 @@ def test_every_declared_symbol_is_exported_and_bound():
     assert set(_lib.SIGNATURES) == set(names)
 
 
+def test_headers_compile_as_c11_and_a_c_caller_links(tmp_path):
+    """What an FFI crate binds: both headers compile as strict C11 (-pedantic
+    -Werror), a C program takes the address of every declared function, links
+    against the library and runs the host-only entry points and an argument
+    error (no GPU call), with the same results as the ctypes binding."""
+    import shutil
+    import subprocess
+
+    import oracle as O
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not found")
+    names = header_functions()
+    src = ["#include \"grout_attn.h\"", "#include \"grout_engine.h\"", "#include <stdio.h>",
+           "typedef void (*fp)(void);", "static fp const table[] = {"]
+    src += [f"    (fp){n}," for n in names]
+    src += ["};",
+            "int main(void) {",
+            "  size_t i;",
+            "  float inv[64];",
+            "  int r;",
+            "  for (i = 0; i < sizeof table / sizeof table[0]; ++i)",
+            "    if (!table[i]) return 10;",
+            "  if (grout_rope_inv_freq(128, 1e6f, inv) != GROUT_OK) return 11;",
+            "  printf(\"%d %d %zu %.9g\\n\", grout_abi_version(),",
+            "         grout_attn_decode_default_splits(32768, 64, 8),",
+            "         grout_attn_decode_workspace_bytes(64, 8, 128, 32), (double)inv[1]);",
+            "  r = grout_fmha_prefill(NULL, NULL, NULL, NULL, 16, 0, 0, 8, 128, 0, 0.1f, NULL);",
+            "  printf(\"%d %s\\n\", r, grout_last_error());",
+            "  return r == GROUT_EINVAL ? 0 : 12;",
+            "}"]
+    (tmp_path / "abi.c").write_text("\n".join(src) + "\n")
+    libdir = os.path.dirname(grout_amd.LIB_PATH)
+    exe = tmp_path / "abi"
+    subprocess.run([gcc, "-std=c11", "-Wall", "-Wextra", "-Werror", "-pedantic",
+                    "-I", os.path.join(ROOT, "include"), str(tmp_path / "abi.c"), "-L", libdir,
+                    "-lgrout_attn", f"-Wl,-rpath,{libdir}", "-o", str(exe)], check=True)
+    run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert run.returncode == 0, (run.returncode, run.stdout, run.stderr)
+    first, second = run.stdout.strip().splitlines()
+    ver, splits, ws, inv1 = first.split()
+    L = grout_amd.lib()
+    assert int(ver) == L.grout_abi_version()
+    assert int(splits) == L.grout_attn_decode_default_splits(32768, 64, 8)
+    assert int(ws) == L.grout_attn_decode_workspace_bytes(64, 8, 128, 32)
+    assert np.float32(float(inv1)) == O.inv_freq(128, 1e6)[1]
+    assert second.startswith("-1 ") and "num_q_heads" in second
+
+
 def test_rope_host_functions_match_oracle_bit_for_bit():
     import oracle as O
 
