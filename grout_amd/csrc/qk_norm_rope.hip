@@ -184,8 +184,9 @@ hipError_t launch_qk_norm_rope_kv_decode(const void* qkv, const void* gamma_q,
                                          void* v_cache, const uint32_t* d_pos, int Hq, int Hkv,
                                          long head_stride, int max_ctx, float eps,
                                          hipStream_t stream) {
-  const dim3 grid(1u, (unsigned)((Hq + Hkv + 7) / 8));
-  qk_norm_rope_kv_kernel<true, 1><<<grid, 256, 0, stream>>>(
+  constexpr int rows = 8 * kRowsPerGroup;  // heads per workgroup
+  const dim3 grid(1u, (unsigned)((Hq + Hkv + rows - 1) / rows));
+  qk_norm_rope_kv_kernel<true, kRowsPerGroup><<<grid, 256, 0, stream>>>(
       (const half_t*)qkv, nullptr, (const half_t*)qkv, (const half_t*)gamma_q,
       (const half_t*)gamma_k, rope_cos, rope_sin, (half_t*)q_out, (half_t*)k_cache,
       (half_t*)v_cache, d_pos, 0, Hq, Hkv, head_stride, max_ctx, eps);

@@ -5,12 +5,11 @@ with the reference's bounds (src/gguf.rs:212-445, its tests at 466-544)."""
 import ctypes as C
 import struct
 
-import numpy as np
 import pytest
 
 import oracle as O
 import qutil
-from gguf_util import (ARRAY, F32, I32, STRING, U8, U32, U64, gguf_bytes, gstr, qwen3_meta,
+from gguf_util import (ARRAY, I32, STRING, U8, U32, U64, gguf_bytes, gstr, qwen3_meta,
                        qwen3_tensors)
 
 Q4, Q5, Q6, Q8, F16 = O.Q4_K, O.Q5_K, O.Q6_K, O.Q8_0, 0
