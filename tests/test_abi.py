@@ -88,6 +88,15 @@ def test_headers_compile_as_c11_and_a_c_caller_links(tmp_path):
     assert second.startswith("-1 ") and "num_q_heads" in second
 
 
+def test_integration_rust_block_declares_every_header_function():
+    """The Rust `extern "C"` block in INTEGRATION.md (what a maintainer would
+    paste into the FFI crate) declares exactly the functions the headers do."""
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    block = text[text.index("## 1."):text.index("## 2.")]
+    declared = set(re.findall(r"pub fn (grout_[a-z0-9_]+)", block))
+    assert declared == set(header_functions())
+
+
 def test_rope_host_functions_match_oracle_bit_for_bit():
     import oracle as O
 
