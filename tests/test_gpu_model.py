@@ -493,6 +493,31 @@ def test_engine_qwen3_4b_shapes_consistency(gpu):
         torch.cuda.empty_cache()
 
 
+def test_engine_qwen3_32b_shapes_consistency(gpu):
+    """Full Qwen3-32B shapes (64 layers, hidden 5120, MLP 25600, 64/8 heads,
+    untied head; 65.5 GB of random N(0, 0.02) fp16 weights): the same
+    decode-at-n equals prefill-of-n+1 property, through the wide GEMVs (K =
+    8192 and 25600) and G = 8 attention."""
+    from grout_amd.model import Engine, Qwen3Config, Qwen3Weights
+
+    cfg = Qwen3Config(64, 5120, 25600, 64, 8, 151936, tie_word_embeddings=False)
+    w = Qwen3Weights.random(cfg, seed=0)
+    eng = Engine(cfg, w, max_ctx=1024)
+    try:
+        prompt = list(np.random.default_rng(32).integers(0, cfg.vocab_size, 18))
+        eng.prefill(prompt)
+        t = 4242
+        step = eng.decode(t).values
+        full = eng.prefill(prompt + [t]).values
+        check_logits(step, full, "32b decode vs prefill")
+        eng.prefill(prompt)
+        assert eng.decode_greedy(t) == int(np.argmax(step))
+    finally:
+        eng.close()
+        del w
+        torch.cuda.empty_cache()
+
+
 # ---------------------------------------------------------------- checkpoint loading
 
 
