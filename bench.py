@@ -306,16 +306,17 @@ def bench_fused_attention(Hq, Hkv, ctx, max_ctx, n_layers, steps, warmup):
     return ms
 
 
-def bench_engine(prompt_len=512, decode_steps=256, max_ctx=1024):
-    """Config 5: Qwen3-4B-shaped engine, random N(0, 0.02) fp16 weights (norm
-    weights 1), a seeded uniform prompt prefilled, then greedy decode steps,
-    each one replay of the captured decode-step graph plus the 4-byte token
-    read-back (the public decode_greedy call, timed on the host clock)."""
+def bench_engine(prompt_len=512, decode_steps=256, max_ctx=1024, cfg=None):
+    """Config 5: Qwen3-4B-shaped engine (or `cfg`), random N(0, 0.02) fp16
+    weights (norm weights 1), a seeded uniform prompt prefilled, then greedy
+    decode steps, each one replay of the captured decode-step graph plus the
+    4-byte token read-back (the public decode_greedy call, timed on the host
+    clock)."""
     import numpy as np
     import torch
     from grout_amd.model import Engine, Qwen3Config, Qwen3Weights
 
-    cfg = Qwen3Config.qwen3_4b()
+    cfg = cfg or Qwen3Config.qwen3_4b()
     w = Qwen3Weights.random(cfg, seed=0)
     eng = Engine(cfg, w, max_ctx=max_ctx)
     prompt = np.random.default_rng(512).integers(0, cfg.vocab_size, prompt_len)
@@ -334,8 +335,10 @@ def bench_engine(prompt_len=512, decode_steps=256, max_ctx=1024):
     decode_s = time.perf_counter() - t0
     eng.close()
     # per decode token: every fp16 weight once (the tied embedding is read as
-    # the lm_head; the embedding gather is one row) + K and V of the live context
-    weight_bytes = 2 * cfg.num_params()
+    # the lm_head; the embedding gather is one row, so an untied embedding
+    # does not count) + K and V of the live context
+    embed_only = 0 if cfg.tie_word_embeddings else cfg.vocab_size * cfg.hidden_size
+    weight_bytes = 2 * (cfg.num_params() - embed_only)
     mean_ctx = prompt_len + decode_steps / 2
     kv_bytes = cfg.num_layers * 2 * cfg.num_key_value_heads * mean_ctx * D * 2
     del w, eng
@@ -343,6 +346,60 @@ def bench_engine(prompt_len=512, decode_steps=256, max_ctx=1024):
     return dict(prefill_ms=prefill_s * 1e3, decode_ms=decode_s * 1e3 / decode_steps,
                 tok_s=decode_steps / decode_s, bytes_per_token=weight_bytes + kv_bytes,
                 distinct_tokens=len(set(toks)), mean_ctx=mean_ctx)
+
+
+# Reference's published request_gen_tps for Qwen3-32B on one B200
+# (benchmarks/RESULTS.md:25-59): (pp, tg) -> grout's median.  Whole-model
+# figures on other hardware: context for the sweep below, not a baseline of
+# this path.
+REFERENCE_32B_B200 = {(18, 36): 79.6, (18, 128): 79.9, (18, 512): 80.1, (128, 36): 79.0,
+                      (512, 36): 75.3, (2048, 36): 61.4, (8192, 36): 37.2}
+
+
+def bench_engine32b(reps=3):
+    """Qwen3-32B-shaped engine (64 layers, hidden 5120, MLP 25600, 64/8 heads,
+    untied head; 65.5 GB of random N(0, 0.02) fp16 weights) driven through
+    the reference's request sweep: each request prefills a seeded uniform
+    prompt of pp tokens (the first generated token) and decodes tg - 1 more
+    greedily; request_gen_tps = tg / end-to-end time, the reference's
+    definition (benchmarks/aggregate_sweep.py:23), median of `reps` requests
+    after one untimed request per prompt length."""
+    import numpy as np
+    import torch
+    from grout_amd.model import Engine, Qwen3Config, Qwen3Weights
+
+    cfg = Qwen3Config(64, 5120, 25600, 64, 8, 151936, tie_word_embeddings=False)
+    w = Qwen3Weights.random(cfg, seed=0)
+    eng = Engine(cfg, w, max_ctx=8192 + 64)
+    rng = np.random.default_rng(512)
+    eng.warmup()
+
+    def request(pp, tg):
+        prompt = rng.integers(0, cfg.vocab_size, pp)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        tok = eng.prefill_greedy(prompt)
+        t1 = time.perf_counter()
+        for _ in range(tg - 1):
+            tok = eng.decode_greedy(tok)
+        t2 = time.perf_counter()
+        return (t1 - t0) * 1e3, (t2 - t0) * 1e3
+
+    out = []
+    for pp, tg in REFERENCE_32B_B200:
+        request(pp, 36 if pp > 18 else 8)  # untimed: rocBLAS picks its kernels per shape
+        runs = sorted((request(pp, tg) for _ in range(reps)), key=lambda r: r[1])
+        pre, e2e = runs[len(runs) // 2]
+        out.append(dict(pp=pp, tg=tg, prefill_ms=round(pre, 2), e2e_ms=round(e2e, 1),
+                        decode_ms_per_token=round((e2e - pre) / (tg - 1), 4),
+                        request_gen_tps=round(tg * 1e3 / e2e, 1),
+                        reference_b200_request_gen_tps=REFERENCE_32B_B200[(pp, tg)]))
+        print(f"# engine32b {out[-1]}", file=sys.stderr, flush=True)
+    eng.close()
+    weight_bytes = 2 * (cfg.num_params() - cfg.vocab_size * cfg.hidden_size)
+    del w, eng
+    torch.cuda.empty_cache()
+    return dict(requests=out, weight_bytes=weight_bytes)
 
 
 def q4km_formats(n_layers, base=12):
@@ -649,6 +706,8 @@ def main():
         res["engine4b"]["attn_graph_ms"] = 36 * bench_fused_attention(
             32, 8, int(res["engine4b"]["mean_ctx"]), 1024, 36, a.steps, a.warmup)
         print(f"# engine4b {res['engine4b']}", file=sys.stderr, flush=True)
+    if want("engine32b"):
+        res["engine32b"] = bench_engine32b()
     if want("engine4b_q4km"):
         res["engine4b_q4km"] = bench_engine_q()
         print(f"# engine4b_q4km {res['engine4b_q4km']}", file=sys.stderr, flush=True)
@@ -734,6 +793,20 @@ def main():
             "weight_stream_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
             "attention_share": round(r["attn_graph_ms"] / r["decode_ms"], 4),
             "attention_us_per_token": round(r["attn_graph_ms"] * 1e3, 1)}
+    if "engine32b" in res:
+        r = res["engine32b"]
+        head = next(q for q in r["requests"] if (q["pp"], q["tg"]) == (18, 128))
+        gbs = r["weight_bytes"] / (head["decode_ms_per_token"] * 1e-3) / 1e9
+        line["engine32b"] = {
+            "workload": "qwen3-32b engine, random N(0,0.02) fp16 weights (untied head); requests "
+                        "of pp prompt tokens + tg generated (greedy, decode-step hipGraph)",
+            "decode_tok_s": round(1e3 / head["decode_ms_per_token"], 1),
+            "decode_ms_per_token": head["decode_ms_per_token"],
+            "weight_stream_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "requests": r["requests"],
+            "reference_context": "reference_b200_request_gen_tps: grout's published medians on "
+                                 "one B200 (benchmarks/RESULTS.md:25-59; whole model, other "
+                                 "hardware)"}
     if "engine4b_q4km" in res:
         r = res["engine4b_q4km"]
         gbs = r["bytes_per_token"] * r["tok_s"] / 1e9
