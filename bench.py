@@ -47,6 +47,20 @@ def parse():
 
 
 GRAPH_TIMING = True
+# Untimed work before every timed region.  After idle the GPU's clocks take
+# ~25 ms of continuous work to settle: S=2048 prefill FMHA measured 47.2, 43.1,
+# 41.2, then 40.0-40.5 us per call over successive 200-call graph replays.
+WARM_MS = 100.0
+
+
+def warm_until(run_once, ms=WARM_MS):
+    """Repeats run_once() (then synchronizes) until `ms` of wall time passed."""
+    import torch
+
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        run_once()
+        torch.cuda.synchronize()
 
 
 def time_launches(fn, steps, warmup, stream=None, graph=None):
@@ -54,7 +68,9 @@ def time_launches(fn, steps, warmup, stream=None, graph=None):
     bracketed by HIP events recorded on the stream the kernels are launched on.
     With graph=True the `steps` calls are first captured into one HIP graph
     (the C ABI calls are capture-safe) so host launch overhead cannot leave the
-    GPU idle between calls; the timed region is one replay of that graph."""
+    GPU idle between calls; the timed region is one replay of that graph.
+    The `warmup` calls and at least WARM_MS of untimed repeats come first, so
+    the timed region runs at settled clocks."""
     import torch
 
     graph = GRAPH_TIMING if graph is None else graph
@@ -68,14 +84,14 @@ def time_launches(fn, steps, warmup, stream=None, graph=None):
         with torch.cuda.graph(g):
             for i in range(steps):
                 fn(i)
-        g.replay()  # untimed replay
-        torch.cuda.synchronize()
+        warm_until(g.replay)  # untimed replays
         s = torch.cuda.current_stream()
         start.record(s)
         g.replay()
         end.record(s)
     else:
         s = stream or torch.cuda.current_stream()
+        warm_until(lambda: [fn(i) for i in range(min(steps, 50))])
         start.record(s)
         for i in range(steps):
             fn(i)
@@ -85,6 +101,36 @@ def time_launches(fn, steps, warmup, stream=None, graph=None):
     if graph:
         del g
     return ms
+
+
+def time_distribution(fn, calls=100, replays=20):
+    """Spread of the per-call device time: `calls` back-to-back calls of fn(i)
+    captured into one HIP graph, replayed `replays` times with a HIP event
+    between consecutive replays on the replaying stream; p10 / median / p90 of
+    the per-call average of each replay, in us (fn must already be warm).
+    Each replay's average also carries the gap before that replay starts
+    (~6.5 us on MI355X), i.e. ~0.07 us per call at 100 calls."""
+    import numpy as np
+    import torch
+
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(calls):
+            fn(i)
+    g.replay()  # untimed replay
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(replays + 1)]
+    ev[0].record(s)
+    for r in range(replays):
+        g.replay()
+        ev[r + 1].record(s)
+    torch.cuda.synchronize()
+    us = np.array([ev[r].elapsed_time(ev[r + 1]) * 1e3 / calls for r in range(replays)])
+    del g
+    p10, med, p90 = np.percentile(us, (10, 50, 90))
+    return dict(p10_us=round(float(p10), 3), median_us=round(float(med), 3),
+                p90_us=round(float(p90), 3), calls_per_replay=calls, replays=replays)
 
 
 class DecodeBench:
@@ -109,7 +155,7 @@ class DecodeBench:
     def alg_bytes(self, ctx):
         return 2 * self.Hkv * ctx * D * 2 + 2 * self.Hq * D * 2
 
-    def time_step(self, ctx, ns, steps, warmup):
+    def time_step(self, ctx, ns, steps, warmup, dist=False):
         import torch
         from grout_amd import ops
 
@@ -121,9 +167,10 @@ class DecodeBench:
             ops.attn_decode(self.q, self.kcs[j], self.vcs[j], pos, num_splits=ns, out=self.out,
                             workspace=ws)
 
-        return time_launches(step, steps, warmup)
+        ms = time_launches(step, steps, warmup)
+        return (ms, time_distribution(step, calls=25 * self.n)) if dist else ms
 
-    def time_split(self, ctx, ns, steps, warmup):
+    def time_split(self, ctx, ns, steps, warmup, dist=False):
         import ctypes as C
         import torch
         from grout_amd import ops
@@ -145,7 +192,8 @@ class DecodeBench:
             call("grout_fmha_decode_gqa_split", qp, kps[j], vps[j], ap, mp, pp, self.Hq,
                  self.Hkv, D, self.max_ctx, self.max_ctx * D, ns, 1.0 / math.sqrt(D), sp)
 
-        return time_launches(split_only, steps, warmup)
+        ms = time_launches(split_only, steps, warmup)
+        return (ms, time_distribution(split_only, calls=25 * self.n)) if dist else ms
 
     def close(self):
         import torch
@@ -179,9 +227,10 @@ def bench_decode32b_sweep(ops, ctxs, steps, warmup, sweep_steps=100):
     for ctx in ctxs:
         sweep = {ns: b.time_step(ctx, ns, sweep_steps, warmup) for ns in DECODE32B_SPLITS}
         best = min(sweep, key=sweep.get)
-        out[ctx] = dict(step_ms=b.time_step(ctx, best, steps, warmup),
-                        split_ms=b.time_split(ctx, best, steps, warmup),
-                        alg_bytes=b.alg_bytes(ctx), num_splits=best,
+        step_ms, step_dist = b.time_step(ctx, best, steps, warmup, dist=True)
+        split_ms, split_dist = b.time_split(ctx, best, steps, warmup, dist=True)
+        out[ctx] = dict(step_ms=step_ms, split_ms=split_ms, step_dist=step_dist,
+                        split_dist=split_dist, alg_bytes=b.alg_bytes(ctx), num_splits=best,
                         default_splits=ops.default_splits(32768, 64, 8),
                         sweep_us={ns: round(ms * 1e3, 2) for ns, ms in sweep.items()})
         print(f"# decode32b ctx={ctx} best={best} {out[ctx]['sweep_us']}", file=sys.stderr,
@@ -221,10 +270,11 @@ def bench_prefill(ops, S, Hq, Hkv, steps, warmup):
     kc = torch.randn((Hkv, S, D), generator=g, device=dev, dtype=torch.float16)
     vc = torch.randn((Hkv, S, D), generator=g, device=dev, dtype=torch.float16)
     out = torch.empty_like(q)
-    ms = time_launches(lambda i=0: ops.fmha_prefill(q, kc, vc, 0, out=out), steps, warmup,
-                       torch.cuda.current_stream(dev))
+    call = lambda i=0: ops.fmha_prefill(q, kc, vc, 0, out=out)
+    ms = time_launches(call, steps, warmup, torch.cuda.current_stream(dev))
     flop = 4.0 * Hq * D * S * (S + 1) / 2
-    return dict(ms=ms, flop=flop, library=bench_prefill_library(q, kc, vc, out, steps, warmup))
+    return dict(ms=ms, flop=flop, dist=time_distribution(call, calls=20),
+                library=bench_prefill_library(q, kc, vc, out, steps, warmup))
 
 
 def bench_prefill_library(q, kc, vc, out, steps, warmup):
@@ -725,7 +775,8 @@ def main():
         line.update(value=round(gbs, 1), unit="GB/s", ms_per_step=round(r["step_ms"], 5))
         line["config"] = {"workload": "qwen3-32b decode attention (split-K + LSE merge), Hq=64 "
                                       "Hkv=8 D=128, ctx 32768, batch 1, 4 rotating layer caches",
-                          "num_splits": r["num_splits"], "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+                          "num_splits": r["num_splits"], "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                          "step_us_dist": r["step_dist"]}
         traffic = DECODE32B_TRAFFIC_BYTES.get(r["num_splits"])
         line["roofline"] = {"bound": "hbm", "kernel": "attn_decode_split_kernel",
                             "achieved": round(split_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -733,6 +784,7 @@ def main():
                             "traffic": traffic,
                             "traffic_source": DECODE32B_TRAFFIC_SOURCE if traffic else None,
                             "kernel_us": round(r["split_ms"] * 1e3, 3),
+                            "kernel_us_dist": r["split_dist"],
                             "alg_bytes_per_launch": r["alg_bytes"]}
         sweep = {}
         for ctx, rr in res["decode32b_sweep"].items():
@@ -742,6 +794,7 @@ def main():
                                "step_gbs": round(g, 1), "step_hbm_frac": round(g / HBM_PEAK_GBS, 4),
                                "split_us": round(rr["split_ms"] * 1e3, 2),
                                "split_gbs": round(sg, 1), "split_hbm_frac": round(sg / HBM_PEAK_GBS, 4),
+                               "step_us_dist": rr["step_dist"], "split_us_dist": rr["split_dist"],
                                "alg_bytes": rr["alg_bytes"], "splits_swept_us": rr["sweep_us"]}
         line["decode32b_sweep"] = sweep
     if "prefill" in res:
@@ -750,12 +803,13 @@ def main():
         line["prefill"] = {"workload": "qwen3-4b causal prefill FMHA S=2048 Hq=32 Hkv=8 D=128",
                            "us": round(r["ms"] * 1e3, 2), "tflops": round(tf, 1),
                            "mfma_frac": round(tf / F16_MFMA_PEAK_TFLOPS, 4),
-                           "flop": r["flop"]}
+                           "flop": r["flop"], "us_dist": r["dist"]}
         sweep = {}
         for S, rr in res["prefill_sweep"].items():
             t = rr["flop"] / (rr["ms"] * 1e-3) / 1e12
             sweep[str(S)] = {"us": round(rr["ms"] * 1e3, 2), "tflops": round(t, 1),
-                             "mfma_frac": round(t / F16_MFMA_PEAK_TFLOPS, 4), "flop": rr["flop"]}
+                             "mfma_frac": round(t / F16_MFMA_PEAK_TFLOPS, 4), "flop": rr["flop"],
+                             "us_dist": rr["dist"]}
             lib = rr.get("library") or {}
             if "ms" in lib:
                 lt = rr["flop"] / (lib["ms"] * 1e-3) / 1e12
