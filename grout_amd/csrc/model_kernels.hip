@@ -156,7 +156,9 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const half_t* __restrict_
 // has its whole share of HBM reads in flight at once.  Partial sums meet in a
 // wave reduction; with a plain input the waves are independent (no LDS, no
 // barrier), with a norm input the workgroup shares x' through LDS
-// (gemv_norm_lds_kernel).  The decode
+// (gemv_norm_lds_kernel), and at the long plain K of the larger models
+// (16-50 chunks) the waves of a workgroup split one row pair's chunks
+// (gemv_splitk_kernel).  The decode
 // shapes compile with CH = the exact chunk count, so no branch separates the
 // loads (a branch there makes the compiler wait for every outstanding load
 // before issuing the next); other K loop over batches of 8 chunks.
@@ -508,6 +510,63 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const half_t* __restri
     gemv_loop<R, IN, OUT>(W, a, y, N, K, gwave, lane);
 }
 
+// Long K, plain input: the W waves of a workgroup share its R rows and split
+// the chunks (wave w takes chunks [w CHW, (w + 1) CHW), k < K; input reads,
+// then all of its weight reads in flight at once); the waves' row sums meet
+// in LDS and are added in wave order.  Measured on MI355X against one wave
+// per row (pair) over the whole K (us, rotating weight copies): 5120 x 25600
+// 40.2 vs 44.1, 5120 x 17408 27.9 vs 31.3, 4096 x 12288 17.2 vs 17.7, 5120 x
+// 8192 14.3 vs 15.2; at 2560 x 9728 and below the one-wave forms stay faster.
+template <int R, int CHW, int W>
+__global__ __launch_bounds__(W * 64) void gemv_splitk_kernel(const half_t* __restrict__ Wm,
+                                                             const half_t* __restrict__ x,
+                                                             half_t* __restrict__ y, int N,
+                                                             int K) {
+  __shared__ float part[W][R];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const half_t* wrow[R];
+  gemv_rows<R, kRows>(Wm, blockIdx.x, N, K, wrow);
+  u32x4 xa[CHW];
+#pragma unroll
+  for (int j = 0; j < CHW; ++j) {
+    const int k = (w * CHW + j) * 512 + lane * 8;
+    xa[j] = load16(x + (k < K ? k : 0));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 wv[CHW][R];
+#pragma unroll
+  for (int j = 0; j < CHW; ++j) {
+    const int k = (w * CHW + j) * 512 + lane * 8;
+#pragma unroll
+    for (int r = 0; r < R; ++r) wv[j][r] = load_stream16(wrow[r] + (k < K ? k : 0));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.f;
+#pragma unroll
+  for (int j = 0; j < CHW; ++j) {
+    const int k = (w * CHW + j) * 512 + lane * 8;
+    const half8 xh = k < K ? as_half8(xa[j]) : half8{};
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = dot8(wv[j][r], xh, acc[r]);
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    acc[r] = wave_sum(acc[r]);
+    if (lane == 0) part[w][r] = acc[r];
+  }
+  __syncthreads();
+  const int row = blockIdx.x * R + lane;
+  if (w == 0 && lane < R && row < N) {
+    float s = part[0][lane];
+#pragma unroll
+    for (int i = 1; i < W; ++i) s += part[i][lane];
+    y[row] = (half_t)s;
+  }
+}
+
 // ------------------------------------------------------------- argmax
 
 constexpr int kArgmaxBlock = 2048;  // logits per first-stage workgroup (256 x 8)
@@ -701,17 +760,32 @@ static hipError_t launch_gemv_mode(const void* W, const GemvArgs& a, void* y, in
   }
   // Long K occurs only for plain inputs (attention width, MLP width).
   if constexpr (IN == kPlain && OUT == kRows) {
+    auto splitk = [&](auto r, auto chw, auto w) {
+      constexpr int R = decltype(r)::value, CHW = decltype(chw)::value,
+                    WV = decltype(w)::value;
+      static_assert(R >= 1 && CHW >= 1 && WV >= 1, "split-K shape");
+      gemv_splitk_kernel<R, CHW, WV><<<(unsigned)((N + R - 1) / R), WV * 64, 0, stream>>>(
+          (const half_t*)W, (const half_t*)a.x, (half_t*)y, N, K);
+      return hipGetLastError();
+    };
+    using I2 = std::integral_constant<int, 2>;
+    using I4 = std::integral_constant<int, 4>;
     switch (nchunks) {
-      // two rows per wave up to 19 chunks (down 2560 x 9728: 9.5 vs 10.3 us
-      // with one row); one at 24, where two would not fit the registers
+      // attention width 8192 (Qwen3-32B o_proj), MLP widths 12288 / 17408 /
+      // 25600 (8B / 14B / 32B down): the chunks split over the waves of a
+      // workgroup
       case 16:
-        gemv_launch<2, IN, OUT, 16>(W, a, y, N, K, stream);
-        return hipGetLastError();
+        return splitk(I2{}, I4{}, I4{});
+      case 24:
+        return splitk(I2{}, std::integral_constant<int, 6>{}, I4{});
+      case 34:
+        return splitk(I2{}, std::integral_constant<int, 17>{}, I2{});
+      case 50:
+        return splitk(I2{}, std::integral_constant<int, 13>{}, I4{});
+      // two rows per wave over the whole K at 19 chunks (down 2560 x 9728:
+      // 9.5 vs 10.3 us with one row; the split forms measured 9.6-10.6)
       case 19:
         gemv_launch<2, IN, OUT, 19>(W, a, y, N, K, stream);
-        return hipGetLastError();
-      case 24:
-        gemv_launch<1, IN, OUT, 24>(W, a, y, N, K, stream);
         return hipGetLastError();
       default:
         break;

@@ -95,8 +95,13 @@ def test_silu_mul(gpu):
     assert np.all(np.abs(O.h2f(host(out)[0, :8])) < 1e-6)
 
 
+# K of 16 / 24 / 34 / 50 chunks of 512 take the split-K kernel (the chunks
+# of a row pair spread over the waves of a workgroup): exact and ragged K,
+# odd N
 @pytest.mark.parametrize("n,k", [(6144, 2560), (2560, 4096), (19456, 2560), (2560, 9728),
-                                 (151936, 2560), (7, 136), (1, 8)])
+                                 (151936, 2560), (7, 136), (1, 8),
+                                 (5, 8192), (17, 7928), (99, 12288), (7, 12280),
+                                 (1001, 17408), (9, 17400), (301, 25600), (33, 25592)])
 def test_gemv(gpu, n, k):
     L = gpu.lib()
     print(f"gemv n={n} k={k}", flush=True)
