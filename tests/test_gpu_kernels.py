@@ -122,6 +122,27 @@ def test_decode_attention_vs_oracle(gpu, Hq, Hkv, ctx, max_ctx, splits):
     _decode_case(gpu, Hq, Hkv, ctx, max_ctx, splits, f"dec{Hq}_{ctx}")
 
 
+def _random_decode_cases(n=12, seed=2024):
+    """Seeded shapes beyond the hand-picked ones: any G <= 16 the decode
+    kernels take, 1-8 kv heads, ragged contexts, caches longer than the
+    context, default or explicit split counts (some above the tile count)."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(n):
+        Hkv = int(rng.choice([1, 2, 4, 8]))
+        G = int(rng.integers(1, 17))
+        ctx = int(rng.integers(1, 3001))
+        max_ctx = ctx + int(rng.integers(0, 65))
+        splits = None if rng.random() < 0.4 else int(rng.integers(1, 65))
+        cases.append((G * Hkv, Hkv, ctx, max_ctx, splits))
+    return cases
+
+
+@pytest.mark.parametrize("Hq,Hkv,ctx,max_ctx,splits", _random_decode_cases())
+def test_decode_random_shapes_vs_oracle(gpu, Hq, Hkv, ctx, max_ctx, splits):
+    _decode_case(gpu, Hq, Hkv, ctx, max_ctx, splits, f"rdec{Hq}_{Hkv}_{ctx}")
+
+
 @pytest.mark.parametrize("Hq,Hkv,pos,max_ctx,splits", [
     (32, 8, 640, 1024, 1),        # engine shape, one split (direct output)
     (32, 8, 640, 1024, None),     # default splits + merge
@@ -239,6 +260,33 @@ def test_prefill_attention_vs_oracle(gpu, S, Hq, Hkv, pos0):
     max_ctx = pos0 + S + 5
     q = normal(f"pq{S}", (S, Hq, D))
     kc, vc = normal(f"pk{S}", (Hkv, max_ctx, D)), normal(f"pv{S}", (Hkv, max_ctx, D))
+    ref = O.attention_prefill_rows(q, kc, vc, pos0, nthreads=8)
+    out = gpu.ops.fmha_prefill(dev(q), dev(kc), dev(vc), pos0)
+    torch.cuda.synchronize()
+    assert_close(host_f32(out), ref, f"prefill S={S} Hq={Hq} Hkv={Hkv} pos0={pos0}")
+
+
+def _random_prefill_cases(n=10, seed=4048):
+    """Seeded prefill shapes: any G up to 16 (head groups of the largest
+    divisor of G that is <= 8), 1-8 kv heads, ragged lengths, and a start
+    position pos0 > 0 in most cases (rows below it come from the cache)."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(n):
+        Hkv = int(rng.choice([1, 2, 4, 8]))
+        G = int(rng.integers(1, 17))
+        S = int(rng.integers(1, 301))
+        pos0 = 0 if rng.random() < 0.3 else int(rng.integers(1, 201))
+        cases.append((S, G * Hkv, Hkv, pos0))
+    return cases
+
+
+@pytest.mark.parametrize("S,Hq,Hkv,pos0", _random_prefill_cases())
+def test_prefill_random_shapes_vs_oracle(gpu, S, Hq, Hkv, pos0):
+    _say("prefill random", S, Hq, Hkv, pos0)
+    max_ctx = pos0 + S + 3
+    q = normal(f"rpq{S}_{Hq}", (S, Hq, D))
+    kc, vc = normal(f"rpk{S}_{Hkv}", (Hkv, max_ctx, D)), normal(f"rpv{S}_{Hkv}", (Hkv, max_ctx, D))
     ref = O.attention_prefill_rows(q, kc, vc, pos0, nthreads=8)
     out = gpu.ops.fmha_prefill(dev(q), dev(kc), dev(vc), pos0)
     torch.cuda.synchronize()
