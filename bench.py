@@ -700,6 +700,23 @@ def cpu_baseline(Hq=64, Hkv=8, ctx=32768, S=2048, pHq=32, pHkv=8):
                  "single_thread_rows": int(len(rows[::8]))})
 
 
+def guarded(fn):
+    """Runs one secondary bench section.  A Python-level failure (out of
+    memory, an argument error) is printed to stderr and returned as
+    {"error": ...}, which the JSON line carries, so the headline measurement
+    still reaches the line.  The headline section itself is not guarded."""
+    import traceback
+
+    import torch
+
+    try:
+        return fn()
+    except Exception as ex:  # noqa: BLE001 - recorded in the line
+        traceback.print_exc()
+        torch.cuda.empty_cache()
+        return {"error": f"{type(ex).__name__}: {ex}"[:400]}
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -730,18 +747,26 @@ def main():
         res["decode32b"] = res["decode32b_sweep"][32768]
         print(f"# decode32b {res['decode32b']}", file=sys.stderr, flush=True)
     if want("prefill"):
-        res["prefill_sweep"] = {S: bench_prefill(ops, S, 32, 8, max(a.steps // (4 if S < 8192 else 10), 10),
-                                                 a.warmup)
-                                for S in (512, 2048, 8192)}
-        res["prefill"] = res["prefill_sweep"][2048]
-        print(f"# prefill {res['prefill_sweep']}", file=sys.stderr, flush=True)
+        sweep = guarded(lambda: {S: bench_prefill(ops, S, 32, 8,
+                                                  max(a.steps // (4 if S < 8192 else 10), 10),
+                                                  a.warmup)
+                                 for S in (512, 2048, 8192)})
+        if "error" in sweep:
+            res["prefill_error"] = sweep
+        else:
+            res["prefill_sweep"] = sweep
+            res["prefill"] = sweep[2048]
+        print(f"# prefill {sweep}", file=sys.stderr, flush=True)
     if want("decode4b"):
-        res["decode4b"] = bench_decode(ops, 32, 8, 4096, 32768, 36, a.steps, a.warmup)
-        res["graph4b_ms"] = bench_decode_graph(grout_amd, 32, 8, 4096, 32768, 36,
+        def decode4b():
+            r = bench_decode(ops, 32, 8, 4096, 32768, 36, a.steps, a.warmup)
+            r["graph_ms"] = bench_decode_graph(grout_amd, 32, 8, 4096, 32768, 36,
                                                max(a.steps // 4, 10), a.warmup)
-        print(f"# decode4b {res['decode4b']} graph {res['graph4b_ms']}", file=sys.stderr, flush=True)
+            return r
+        res["decode4b"] = guarded(decode4b)
+        print(f"# decode4b {res['decode4b']}", file=sys.stderr, flush=True)
     if want("norm"):
-        res["norm"] = bench_norm(ops, 2048, 32, 8, 32768, a.steps, a.warmup)
+        res["norm"] = guarded(lambda: bench_norm(ops, 2048, 32, 8, 32768, a.steps, a.warmup))
         print(f"# norm {res['norm']}", file=sys.stderr, flush=True)
     if "gemv" in only:
         res["gemv"] = bench_gemv(a.steps, a.warmup)
@@ -750,19 +775,22 @@ def main():
         res["qgemv"] = bench_qgemv(a.steps, a.warmup)
         print(f"# qgemv {res['qgemv']}", file=sys.stderr, flush=True)
     if want("engine4b"):
-        res["engine4b"] = bench_engine()
-        # attention part of one decode step at the mean context of the run:
-        # 36 layers of the fused norm/RoPE/KV write + split-K + merge
-        res["engine4b"]["attn_graph_ms"] = 36 * bench_fused_attention(
-            32, 8, int(res["engine4b"]["mean_ctx"]), 1024, 36, a.steps, a.warmup)
+        def engine4b():
+            r = bench_engine()
+            # attention part of one decode step at the mean context of the run:
+            # 36 layers of the fused norm/RoPE/KV write + split-K + merge
+            r["attn_graph_ms"] = 36 * bench_fused_attention(
+                32, 8, int(r["mean_ctx"]), 1024, 36, a.steps, a.warmup)
+            return r
+        res["engine4b"] = guarded(engine4b)
         print(f"# engine4b {res['engine4b']}", file=sys.stderr, flush=True)
     if want("engine32b"):
-        res["engine32b"] = bench_engine32b()
+        res["engine32b"] = guarded(bench_engine32b)
     if want("engine4b_q4km"):
-        res["engine4b_q4km"] = bench_engine_q()
+        res["engine4b_q4km"] = guarded(bench_engine_q)
         print(f"# engine4b_q4km {res['engine4b_q4km']}", file=sys.stderr, flush=True)
     if "engine4b_q5km" in only:
-        res["engine4b_q5km"] = bench_engine_q(base=13)
+        res["engine4b_q5km"] = guarded(lambda: bench_engine_q(base=13))
         print(f"# engine4b_q5km {res['engine4b_q5km']}", file=sys.stderr, flush=True)
 
     line = {"metric": "decode-attn HBM GB/s (% of peak) + prefill FMHA TFLOP/s (% MFMA peak)",
@@ -797,7 +825,10 @@ def main():
                                "step_us_dist": rr["step_dist"], "split_us_dist": rr["split_dist"],
                                "alg_bytes": rr["alg_bytes"], "splits_swept_us": rr["sweep_us"]}
         line["decode32b_sweep"] = sweep
-    if "prefill" in res:
+    def ok(key):
+        return key in res and "error" not in res[key]
+
+    if ok("prefill"):
         r = res["prefill"]
         tf = r["flop"] / (r["ms"] * 1e-3) / 1e12
         line["prefill"] = {"workload": "qwen3-4b causal prefill FMHA S=2048 Hq=32 Hkv=8 D=128",
@@ -819,14 +850,14 @@ def main():
             elif lib:
                 sweep[str(S)]["library"] = lib
         line["prefill_sweep"] = sweep
-    if "decode4b" in res:
+    if ok("decode4b"):
         r = res["decode4b"]
         gbs = r["alg_bytes"] / (r["step_ms"] * 1e-3) / 1e9
         line["decode4b"] = {"workload": "qwen3-4b decode attention Hq=32 Hkv=8 ctx 4096, 36 layer caches",
                             "us_per_layer": round(r["step_ms"] * 1e3, 2), "gbs": round(gbs, 1),
                             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "num_splits": r["num_splits"],
-                            "graph_36_layers_us": round(res["graph4b_ms"] * 1e3, 1)}
-    if "norm" in res:
+                            "graph_36_layers_us": round(r["graph_ms"] * 1e3, 1)}
+    if ok("norm"):
         r = res["norm"]
         gbs = r["alg_bytes"] / (r["ms"] * 1e-3) / 1e9
         line["qk_norm_rope_kv"] = {"workload": "fused QK-norm/RoPE/KV write S=2048 Hq=32 Hkv=8",
@@ -836,7 +867,7 @@ def main():
         line["gemv"] = res["gemv"]
     if "qgemv" in res:
         line["qgemv"] = res["qgemv"]
-    if "engine4b" in res:
+    if ok("engine4b"):
         r = res["engine4b"]
         gbs = r["bytes_per_token"] * r["tok_s"] / 1e9
         line["engine4b"] = {
@@ -847,7 +878,7 @@ def main():
             "weight_stream_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
             "attention_share": round(r["attn_graph_ms"] / r["decode_ms"], 4),
             "attention_us_per_token": round(r["attn_graph_ms"] * 1e3, 1)}
-    if "engine32b" in res:
+    if ok("engine32b"):
         r = res["engine32b"]
         head = next(q for q in r["requests"] if (q["pp"], q["tg"]) == (18, 128))
         gbs = r["weight_bytes"] / (head["decode_ms_per_token"] * 1e-3) / 1e9
@@ -861,7 +892,7 @@ def main():
             "reference_context": "reference_b200_request_gen_tps: grout's published medians on "
                                  "one B200 (benchmarks/RESULTS.md:25-59; whole model, other "
                                  "hardware)"}
-    if "engine4b_q4km" in res:
+    if ok("engine4b_q4km"):
         r = res["engine4b_q4km"]
         gbs = r["bytes_per_token"] * r["tok_s"] / 1e9
         line["engine4b_q4km"] = {
@@ -872,7 +903,7 @@ def main():
             "prefill_512_ms": round(r["prefill_ms"], 2),
             "weight_bytes": r["weight_bytes"],
             "weight_stream_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
-    if "engine4b_q5km" in res:
+    if ok("engine4b_q5km"):
         r = res["engine4b_q5km"]
         gbs = r["bytes_per_token"] * r["tok_s"] / 1e9
         line["engine4b_q5km"] = {
@@ -883,8 +914,13 @@ def main():
             "prefill_512_ms": round(r["prefill_ms"], 2),
             "weight_bytes": r["weight_bytes"],
             "weight_stream_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    # sections that failed carry their error instead of numbers
+    names = {"prefill_error": "prefill", "norm": "qk_norm_rope_kv"}
+    for key, v in res.items():
+        if isinstance(v, dict) and "error" in v:
+            line[names.get(key, key)] = v
     if not a.no_cpu and "decode32b" in res:
-        cb = cpu_baseline()
+        cb = guarded(cpu_baseline)
 
         def rnd(v):
             if isinstance(v, float):

@@ -13,3 +13,13 @@ def test_bench_refuses_more_than_one_gpu():
     assert r.returncode == 2, r.stderr
     assert "one GPU" in r.stderr
     assert r.stdout == ""
+
+
+def test_guarded_section_records_its_error():
+    # a secondary section that raises leaves an error entry, not a missing line
+    sys.path.insert(0, ROOT)
+    import bench
+
+    assert bench.guarded(lambda: {"us": 1.0}) == {"us": 1.0}
+    r = bench.guarded(lambda: 1 / 0)
+    assert r == {"error": "ZeroDivisionError: division by zero"}
