@@ -523,6 +523,35 @@ def test_engine_qwen3_32b_shapes_consistency(gpu):
         torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("name,layers,hidden,inter,hq", [
+    ("8b", 36, 4096, 12288, 32),    # down K = 12288: 24 chunks, split over 4 waves
+    ("14b", 40, 5120, 17408, 40),   # down K = 17408: 34 chunks over 2 waves; G = 5
+])
+def test_engine_qwen3_8b_14b_shapes_consistency(gpu, name, layers, hidden, inter, hq):
+    """Qwen3-8B / 14B shapes (8 kv heads, untied head, random N(0, 0.02) fp16
+    weights): decode at n equals a prefill of n + 1 (library GEMMs) through
+    the split-K long-K GEMVs and the norm-fused GEMVs at hidden 4096 / 5120."""
+    from grout_amd.model import Engine, Qwen3Config, Qwen3Weights
+
+    cfg = Qwen3Config(layers, hidden, inter, hq, 8, 151936, tie_word_embeddings=False)
+    w = Qwen3Weights.random(cfg, seed=1)
+    eng = Engine(cfg, w, max_ctx=512)
+    try:
+        print(f"[case] engine {name}", flush=True)
+        prompt = list(np.random.default_rng(14).integers(0, cfg.vocab_size, 21))
+        eng.prefill(prompt)
+        t = 777
+        step = eng.decode(t).values
+        full = eng.prefill(prompt + [t]).values
+        check_logits(step, full, f"{name} decode vs prefill")
+        eng.prefill(prompt)
+        assert eng.decode_greedy(t) == int(np.argmax(step))
+    finally:
+        eng.close()
+        del w
+        torch.cuda.empty_cache()
+
+
 # ---------------------------------------------------------------- checkpoint loading
 
 
