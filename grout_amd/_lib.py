@@ -129,7 +129,9 @@ SIGNATURES = {
     "grout_engine_decode": (_i, [_p, _u32, _p]),
     "grout_engine_decode_greedy": (_i, [_p, _u32, _p]),
     "grout_engine_reset": (_i, [_p]),
+    "grout_engine_warmup": (_i, [_p]),
     "grout_engine_position": (_i, [_p]),
+    "grout_env_flag": (_i, [C.c_char_p, _i]),
     "grout_engine_vram_preflight": (_i, [C.POINTER(Qwen3Config), _sz, _sz, _sz, _sz,
                                          C.POINTER(_sz)]),
     "grout_engine_uses_decode_graph": (_i, [_p]),

@@ -88,4 +88,22 @@ inline size_t decode_ws_bytes(int hq, int hkv, int nsplit) {
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// A boolean switch's value as the reference's env_bool_or reads one
+// (src/model.rs:212-224): surrounding whitespace trimmed, case ignored,
+// "1"/"true"/"on"/"yes" on, "0"/"false"/"off"/"no"/"" off, anything else (or
+// an unset variable, raw == NULL) the default.
+inline bool parse_bool_or(const char* raw, bool dflt) {
+  if (raw == nullptr) return dflt;
+  std::string v(raw);
+  const char* ws = " \t\n\r\f\v";
+  const size_t b = v.find_first_not_of(ws);
+  if (b == std::string::npos) return false;
+  v = v.substr(b, v.find_last_not_of(ws) - b + 1);
+  for (char& c : v)
+    if (c >= 'A' && c <= 'Z') c = (char)(c - 'A' + 'a');
+  if (v == "1" || v == "true" || v == "on" || v == "yes") return true;
+  if (v == "0" || v == "false" || v == "off" || v == "no") return false;
+  return dflt;
+}
+
 }  // namespace grout_abi

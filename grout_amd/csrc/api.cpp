@@ -206,12 +206,17 @@ int grout_attn_decode(const void* q, const void* k_cache, const void* v_cache, v
                     "attn_decode merge launch");
 }
 
-int grout_attn_decode_fused(const void* qkv, const void* gamma_q, const void* gamma_k,
-                            const float* rope_cos, const float* rope_sin, void* k_cache,
-                            void* v_cache, void* out, void* workspace, size_t workspace_bytes,
-                            const uint32_t* d_pos, int num_q_heads, int num_kv_heads,
-                            int head_dim, int max_ctx, long kv_head_stride, int num_splits,
-                            float eps, float qk_scale, void* stream) {
+}  // extern "C"
+
+// grout_attn_decode_fused, plus the captured decode graph's option of having
+// the merge of its last layer move the position word on (advance_pos).
+static int attn_decode_fused_impl(const void* qkv, const void* gamma_q, const void* gamma_k,
+                                  const float* rope_cos, const float* rope_sin, void* k_cache,
+                                  void* v_cache, void* out, void* workspace,
+                                  size_t workspace_bytes, const uint32_t* d_pos,
+                                  int num_q_heads, int num_kv_heads, int head_dim, int max_ctx,
+                                  long kv_head_stride, int num_splits, float eps, float qk_scale,
+                                  void* stream, uint32_t* advance_pos) {
   GROUT_CHECK(check_heads(num_q_heads, num_kv_heads, head_dim, kMaxDecodeGroup));
   if (num_splits <= 0) num_splits = grout_attn_decode_default_splits(max_ctx, num_q_heads, num_kv_heads);
   GROUT_NEED(num_splits <= kMaxSplits, GROUT_EINVAL, "num_splits=%d > %d", num_splits, kMaxSplits);
@@ -239,8 +244,22 @@ int grout_attn_decode_fused(const void* qkv, const void* gamma_q, const void* ga
                                                     k_cache, v_cache, kv_head_stride, d_pos,
                                                     max_ctx, num_q_heads, num_kv_heads,
                                                     num_splits, eps, qk_scale, part_acc, part_ml,
-                                                    out, as_stream(stream)),
+                                                    out, as_stream(stream), advance_pos),
                     "attn_decode_fused launch");
+}
+
+extern "C" {
+
+int grout_attn_decode_fused(const void* qkv, const void* gamma_q, const void* gamma_k,
+                            const float* rope_cos, const float* rope_sin, void* k_cache,
+                            void* v_cache, void* out, void* workspace, size_t workspace_bytes,
+                            const uint32_t* d_pos, int num_q_heads, int num_kv_heads,
+                            int head_dim, int max_ctx, long kv_head_stride, int num_splits,
+                            float eps, float qk_scale, void* stream) {
+  return attn_decode_fused_impl(qkv, gamma_q, gamma_k, rope_cos, rope_sin, k_cache, v_cache, out,
+                                workspace, workspace_bytes, d_pos, num_q_heads, num_kv_heads,
+                                head_dim, max_ctx, kv_head_stride, num_splits, eps, qk_scale,
+                                stream, nullptr);
 }
 
 }  // extern "C"
@@ -327,6 +346,10 @@ struct grout_decode_graph {
   hipGraphExec_t exec = nullptr;
   uint32_t* d_pos = nullptr;
   int max_ctx = 0;
+  // The last layer's merge leaves position + 1 in d_pos (split count > 1):
+  // a launch at that position needs no write of its own.  -1: unknown.
+  bool advances = false;
+  long next_pos = -1;
 };
 
 }  // extern "C"
@@ -377,13 +400,16 @@ int grout_decode_graph_create(const grout_decode_layer* layers, int num_layers,
   if (rc == GROUT_OK) {
     rc = hip_status(hipStreamBeginCapture(cap, hipStreamCaptureModeThreadLocal), "BeginCapture");
     if (rc == GROUT_OK) {
-      // Per layer: the fused norm/RoPE/KV write + split-K pass, then the merge.
+      // Per layer: the fused norm/RoPE/KV write + split-K pass, then the
+      // merge; the last merge moves the position word on to the next step's.
+      g->advances = num_splits > 1;
       for (int i = 0; i < num_layers && rc == GROUT_OK; ++i) {
         const grout_decode_layer& L = layers[i];
-        rc = grout_attn_decode_fused(L.qkv, L.gamma_q, L.gamma_k, rope_cos, rope_sin, L.k_cache,
-                                     L.v_cache, L.attn_out, workspace, workspace_bytes, g->d_pos,
-                                     num_q_heads, num_kv_heads, head_dim, max_ctx, stride,
-                                     num_splits, eps, qk_scale, cap);
+        rc = attn_decode_fused_impl(L.qkv, L.gamma_q, L.gamma_k, rope_cos, rope_sin, L.k_cache,
+                                    L.v_cache, L.attn_out, workspace, workspace_bytes, g->d_pos,
+                                    num_q_heads, num_kv_heads, head_dim, max_ctx, stride,
+                                    num_splits, eps, qk_scale, cap,
+                                    i + 1 == num_layers && g->advances ? g->d_pos : nullptr);
       }
       hipGraph_t graph = nullptr;
       const hipError_t e = hipStreamEndCapture(cap, &graph);
@@ -409,11 +435,20 @@ int grout_decode_graph_launch(grout_decode_graph* graph, uint32_t position, void
   GROUT_NEED(graph != nullptr && graph->exec != nullptr, GROUT_EINVAL, "graph is NULL");
   GROUT_NEED((long)position < (long)graph->max_ctx, GROUT_EINVAL,
              "decode position %u exceeds max_ctx=%d", position, graph->max_ctx);
-  // The position travels as a kernel argument, so queued launches never race
-  // on a host staging buffer.
-  set_position_kernel<<<1, 1, 0, as_stream(stream)>>>(graph->d_pos, position);
-  GROUT_CHECK(hip_status(hipGetLastError(), "set position"));
-  return hip_status(hipGraphLaunch(graph->exec, as_stream(stream)), "hipGraphLaunch");
+  // Consecutive steps (position = the previous launch's + 1) find the word
+  // already moved on by the previous replay: one hipGraphLaunch per step.
+  // Any other position is written first by a one-thread kernel whose
+  // argument carries it, so queued launches never race on a host staging
+  // buffer.
+  if (!(graph->advances && (long)position == graph->next_pos)) {
+    graph->next_pos = -1;
+    set_position_kernel<<<1, 1, 0, as_stream(stream)>>>(graph->d_pos, position);
+    GROUT_CHECK(hip_status(hipGetLastError(), "set position"));
+  }
+  graph->next_pos = -1;
+  GROUT_CHECK(hip_status(hipGraphLaunch(graph->exec, as_stream(stream)), "hipGraphLaunch"));
+  graph->next_pos = (long)position + 1;
+  return GROUT_OK;
 }
 
 const uint32_t* grout_decode_graph_position_ptr(const grout_decode_graph* graph) {

@@ -422,7 +422,10 @@ constexpr int kMergeGroups = 8;
 
 __global__ __launch_bounds__(128) void attn_decode_merge_kernel(
     const float* __restrict__ part_acc, const float* __restrict__ part_ml,
-    half_t* __restrict__ out, int G, int nsplit) {
+    half_t* __restrict__ out, int G, int nsplit, uint32_t* __restrict__ advance_pos) {
+  // The split pass that precedes this launch has read the position: this
+  // kernel never does, so it may move the word on to the next step's.
+  if (advance_pos != nullptr && blockIdx.x == 0 && threadIdx.x == 0) advance_pos[0] += 1u;
   __shared__ float s_m[kMergeGroups][16];
   __shared__ float s_l[kMergeGroups][16];
   __shared__ floatx4 s_o[kMergeGroups][16];
@@ -486,7 +489,7 @@ hipError_t launch_attn_decode_fused(const void* qkv, const void* gamma_q, const 
                                     void* v_cache, long head_stride, const uint32_t* d_pos,
                                     int max_ctx, int Hq, int Hkv, int nsplit, float eps,
                                     float qk_scale, float* part_acc, float* part_ml, void* out,
-                                    hipStream_t stream) {
+                                    hipStream_t stream, uint32_t* advance_pos) {
   const float scale_log2 = qk_scale * 1.4426950408889634f;
   const DecodeFused fz{(const half_t*)qkv, (const half_t*)gamma_q, (const half_t*)gamma_k,
                        rope_cos, rope_sin, (half_t*)k_cache, (half_t*)v_cache, eps, Hq};
@@ -504,13 +507,14 @@ hipError_t launch_attn_decode_fused(const void* qkv, const void* gamma_q, const 
           Hq / Hkv, nsplit, scale_log2, part_acc, part_ml, fz, nullptr);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  return launch_attn_decode_merge(part_acc, part_ml, out, Hq, Hkv, nsplit, stream);
+  return launch_attn_decode_merge(part_acc, part_ml, out, Hq, Hkv, nsplit, stream, advance_pos);
 }
 
 hipError_t launch_attn_decode_merge(const float* part_acc, const float* part_ml, void* out,
-                                    int Hq, int Hkv, int nsplit, hipStream_t stream) {
-  attn_decode_merge_kernel<<<(unsigned)(2 * Hq), 128, 0, stream>>>(part_acc, part_ml,
-                                                                      (half_t*)out, Hq / Hkv, nsplit);
+                                    int Hq, int Hkv, int nsplit, hipStream_t stream,
+                                    uint32_t* advance_pos) {
+  attn_decode_merge_kernel<<<(unsigned)(2 * Hq), 128, 0, stream>>>(
+      part_acc, part_ml, (half_t*)out, Hq / Hkv, nsplit, advance_pos);
   return hipGetLastError();
 }
 

@@ -146,6 +146,10 @@ struct grout_engine {
 
   int next_pos = 0;
   bool session_active = false;
+  // What the device's decode token / position words hold, as far as the host
+  // knows (-1: unknown).  Each decode step leaves its argmax and position + 1
+  // there; a step whose token and position match needs no write.
+  long dev_token = -1, dev_pos = -1;
   std::string pending_reset_error;
 
   // Set by grout_engine_load: the checkpoint's weights, freed with the engine.
@@ -244,15 +248,17 @@ int norm(grout_engine* e, const void* residual, const void* x, const void* w, vo
 }
 
 // Final norm (folding the last layer's residual add), lm_head and argmax
-// over one token's hidden state; leaves f16 logits and the token on device.
-int head(grout_engine* e, const void* hidden_after_attn, const void* ff_down) {
+// over one token's hidden state; leaves f16 logits and the token on device
+// (and, when advance_pos is set, moves that position word on by one).
+int head(grout_engine* e, const void* hidden_after_attn, const void* ff_down,
+         uint32_t* advance_pos = nullptr) {
   const auto& c = e->cfg;
   GROUT_CHECK(norm(e, hidden_after_attn, ff_down, e->final_norm, e->d(e->db.normed),
                    e->d(e->db.hidden), 1));
   GROUT_CHECK(mat_gemv(e, e->lm_head, e->d(e->db.normed), e->d(e->db.logits), c.hidden_size));
   return hip_status(grout::launch_argmax(e->d(e->db.logits), e->d<float>(e->db.argmax_max),
                                          e->d<uint32_t>(e->db.argmax_idx), c.vocab_size,
-                                         e->d<uint32_t>(e->db.token), e->stream),
+                                         e->d<uint32_t>(e->db.token), e->stream, advance_pos),
                     "argmax");
 }
 
@@ -318,7 +324,9 @@ int record_decode_step(grout_engine* e) {
     }
     GROUT_CHECK(mat_gemv(e, w.down, e->d(b.ff), e->d(b.ff_down), I));
   }
-  return head(e, e->d(b.hidden_after_attn), e->d(b.ff_down));
+  // The step leaves the next step's token (the greedy argmax) and position
+  // behind, so a greedy decode loop needs no write of its own per token.
+  return head(e, e->d(b.hidden_after_attn), e->d(b.ff_down), e->d<uint32_t>(b.pos));
 }
 
 int capture_decode_graph(grout_engine* e) {
@@ -335,14 +343,15 @@ int capture_decode_graph(grout_engine* e) {
                     "hipGraphInstantiate");
 }
 
-// The decode-step graph, or the sequential fallback: GROUT_HIP_GRAPH_DECODE=0
+// The decode-step graph, or the sequential fallback: GROUT_HIP_GRAPH_DECODE
+// set off (read like the reference's GROUT_CUDA_GRAPH_DECODE, default on)
 // skips the capture, and a failed capture is reported on stderr and recorded
 // (src/model.rs:1700-1701, 2130-2145, 2300-2309).  Either way decode then
 // launches record_decode_step's kernels directly, in the same order.
 int setup_decode_graph(grout_engine* e) {
   const char* env = std::getenv("GROUT_HIP_GRAPH_DECODE");
-  if (env && std::strcmp(env, "0") == 0) {
-    e->graph_error = "decode graph disabled by GROUT_HIP_GRAPH_DECODE=0";
+  if (!parse_bool_or(env, true)) {
+    e->graph_error = std::string("decode graph disabled by GROUT_HIP_GRAPH_DECODE=") + env;
     return GROUT_OK;
   }
   if (capture_decode_graph(e) == GROUT_OK) return GROUT_OK;
@@ -434,16 +443,24 @@ int decode_common(grout_engine* e, uint32_t token) {
   GROUT_NEED(token < (uint32_t)e->cfg.vocab_size, GROUT_EINVAL, "token %u >= vocab_size=%d",
              token, e->cfg.vocab_size);
   GROUT_CHECK(hip_status(hipSetDevice(e->device), "hipSetDevice"));
-  // Token and position travel as kernel arguments: no host staging buffer
-  // that a queued replay could still be reading.
-  set_step_kernel<<<1, 1, 0, e->stream>>>(e->d<uint32_t>(e->db.token), token,
-                                          e->d<uint32_t>(e->db.pos), (uint32_t)e->next_pos);
-  GROUT_CHECK(hip_status(hipGetLastError(), "set step"));
+  // The previous step left its greedy token and this position on the device
+  // (the usual decode_greedy loop): one graph launch.  Otherwise token and
+  // position travel as kernel arguments of a one-thread kernel first: no host
+  // staging buffer that a queued replay could still be reading.
+  const bool ready = e->dev_token == (long)token && e->dev_pos == (long)e->next_pos;
+  e->dev_token = -1;
+  e->dev_pos = -1;
+  if (!ready) {
+    set_step_kernel<<<1, 1, 0, e->stream>>>(e->d<uint32_t>(e->db.token), token,
+                                            e->d<uint32_t>(e->db.pos), (uint32_t)e->next_pos);
+    GROUT_CHECK(hip_status(hipGetLastError(), "set step"));
+  }
   if (e->exec)
     GROUT_CHECK(hip_status(hipGraphLaunch(e->exec, e->stream), "hipGraphLaunch"));
   else
     GROUT_CHECK(record_decode_step(e));
   e->next_pos += 1;
+  e->dev_pos = e->next_pos;
   return GROUT_OK;
 }
 
@@ -750,6 +767,25 @@ int grout_gemv(const void* W, const void* x, void* y, int n, int k, void* stream
   return hip_status(grout::launch_gemv(W, x, y, n, k, as_stream(stream)), "gemv launch");
 }
 
+// True when the byte ranges [a, a + an) and [b, b + bn) share a byte.
+static bool ranges_overlap(const void* a, size_t an, const void* b, size_t bn) {
+  if (a == nullptr || b == nullptr || an == 0 || bn == 0) return false;
+  const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+  return pa < pb + bn && pb < pa + an;
+}
+
+// One workgroup of the fused-norm GEMVs writes residual_out[0, k) while the
+// others still read residual and x: any overlap of those f16 vectors races,
+// not only the same start address.
+static int check_residual_out(const void* residual, const void* x, const void* residual_out,
+                              int k) {
+  const size_t bytes = (size_t)k * sizeof(uint16_t);
+  GROUT_NEED(!ranges_overlap(residual_out, bytes, residual, bytes) &&
+                 !ranges_overlap(residual_out, bytes, x, bytes),
+             GROUT_EINVAL, "residual_out must not overlap residual or x");
+  return GROUT_OK;
+}
+
 static int check_gemv_norm(const void* W, const void* residual, const void* x,
                            const void* gamma, void* residual_out, void* y, int n, int k,
                            float eps) {
@@ -757,10 +793,7 @@ static int check_gemv_norm(const void* W, const void* residual, const void* x,
   GROUT_CHECK(check_norm(1, k, eps));
   GROUT_CHECK(check_ptrs16({{W, "W"}, {x, "x"}, {gamma, "gamma"}}));
   if (residual) GROUT_CHECK(check_ptrs16({{residual, "residual"}, {residual_out, "residual_out"}}));
-  // One workgroup writes residual_out while the others still read residual
-  // and x: in-place use would race.
-  GROUT_NEED(residual_out == nullptr || (residual_out != residual && residual_out != x),
-             GROUT_EINVAL, "residual_out must not alias residual or x");
+  GROUT_CHECK(check_residual_out(residual, x, residual_out, k));
   GROUT_NEED(y != nullptr && (reinterpret_cast<uintptr_t>(y) & 1u) == 0, GROUT_EALIGN,
              "y is NULL or not 2-byte aligned");
   return GROUT_OK;
@@ -825,13 +858,12 @@ int grout_gemv_q_silu_mul(int fmt, const void* wq, const void* x, void* y, int i
 }
 
 static int check_q_norm(const void* wq, const void* residual, const void* x, const void* gamma,
-                        const void* residual_out, const void* y, float eps) {
+                        const void* residual_out, const void* y, int k, float eps) {
   GROUT_CHECK(check_ptrs16({{wq, "wq"}, {x, "x"}, {gamma, "gamma"}}));
   if (residual) GROUT_CHECK(check_ptrs16({{residual, "residual"}}));
   if (residual_out) {
     GROUT_CHECK(check_ptrs16({{residual_out, "residual_out"}}));
-    GROUT_NEED(residual_out != residual && residual_out != x, GROUT_EINVAL,
-               "residual_out must not alias residual or x");
+    GROUT_CHECK(check_residual_out(residual, x, residual_out, k));
   }
   GROUT_NEED(y != nullptr && (reinterpret_cast<uintptr_t>(y) & 1u) == 0, GROUT_EALIGN,
              "y is NULL or not 2-byte aligned");
@@ -843,7 +875,7 @@ int grout_gemv_q_rms_norm(int fmt, const void* wq, const void* residual, const v
                           const void* gamma, void* residual_out, void* y, int n, int k, float eps,
                           void* stream) {
   GROUT_CHECK(check_q(fmt, n, k));
-  GROUT_CHECK(check_q_norm(wq, residual, x, gamma, residual_out, y, eps));
+  GROUT_CHECK(check_q_norm(wq, residual, x, gamma, residual_out, y, k, eps));
   return hip_status(grout::launch_gemv_q_norm(fmt, wq, residual, x, gamma, residual_out, eps, y, n,
                                               k, false, as_stream(stream)),
                     "gemv_q_rms_norm launch");
@@ -853,7 +885,7 @@ int grout_gemv_q_rms_norm_silu_mul(int fmt, const void* wq, const void* residual
                                    const void* gamma, void* residual_out, void* y, int inter,
                                    int k, float eps, void* stream) {
   GROUT_CHECK(check_q(fmt, 2 * inter, k));
-  GROUT_CHECK(check_q_norm(wq, residual, x, gamma, residual_out, y, eps));
+  GROUT_CHECK(check_q_norm(wq, residual, x, gamma, residual_out, y, k, eps));
   return hip_status(grout::launch_gemv_q_norm(fmt, wq, residual, x, gamma, residual_out, eps, y,
                                               inter, k, true, as_stream(stream)),
                     "gemv_q_rms_norm_silu_mul launch");
@@ -963,6 +995,8 @@ int run_chunk(grout_engine* e, const uint32_t* tokens, int n, int pos0, float* l
                "token %u at %d >= vocab_size=%d", tokens[i], i, c.vocab_size);
   GROUT_CHECK(hip_status(hipSetDevice(e->device), "hipSetDevice"));
   e->session_active = false;
+  e->dev_token = -1;  // the prefill's head writes the token word
+  e->dev_pos = -1;
   GROUT_CHECK(ensure_prefill_capacity(e, n));
   const PrefillBufs& b = e->pb;
   hipStream_t s = e->stream;
@@ -1049,20 +1083,27 @@ int grout_engine_extend(grout_engine* e, const uint32_t* tokens, int n, float* l
 int grout_engine_decode(grout_engine* e, uint32_t token, float* logits_out) {
   GROUT_NEED(e != nullptr, GROUT_EINVAL, "engine is NULL");
   GROUT_CHECK(decode_common(e, token));
-  return copy_logits_out(e, logits_out, nullptr);
+  uint32_t greedy = 0;  // 4 more bytes in the same read-back
+  GROUT_CHECK(copy_logits_out(e, logits_out, &greedy));
+  e->dev_token = greedy;
+  return GROUT_OK;
 }
 
 int grout_engine_decode_greedy(grout_engine* e, uint32_t token, uint32_t* next_token) {
   GROUT_NEED(e != nullptr, GROUT_EINVAL, "engine is NULL");
   GROUT_NEED(next_token != nullptr, GROUT_EINVAL, "next_token is NULL");
   GROUT_CHECK(decode_common(e, token));
-  return copy_logits_out(e, nullptr, next_token);
+  GROUT_CHECK(copy_logits_out(e, nullptr, next_token));
+  e->dev_token = *next_token;
+  return GROUT_OK;
 }
 
 int grout_engine_reset(grout_engine* e) {
   GROUT_NEED(e != nullptr, GROUT_EINVAL, "engine is NULL");
   e->next_pos = 0;
   e->session_active = false;
+  e->dev_token = -1;
+  e->dev_pos = -1;
   int rc = hip_status(hipSetDevice(e->device), "hipSetDevice");
   if (rc == GROUT_OK)
     rc = hip_status(
@@ -1076,7 +1117,37 @@ int grout_engine_reset(grout_engine* e) {
   return GROUT_OK;
 }
 
+int grout_engine_warmup(grout_engine* e) {
+  GROUT_NEED(e != nullptr, GROUT_EINVAL, "engine is NULL");
+  GROUT_CHECK(take_pending(e));
+  // The model's first stop token, else 0 (src/api.rs:153-162).
+  uint32_t token = 0;
+  grout_model_info info{};
+  if (e->owned_model && grout_model_get_info(e->owned_model, &info) == GROUT_OK &&
+      info.num_eos > 0)
+    token = info.eos_token_ids[0];
+  GROUT_NEED(token < (uint32_t)e->cfg.vocab_size, GROUT_EINVAL,
+             "warmup token %u >= vocab_size=%d", token, e->cfg.vocab_size);
+  // One-token steps at positions 0 and 1 (src/model.rs:2204-2212): the
+  // prefill path (library GEMMs, prefill kernels) and one decode-graph
+  // replay, then the caches are zeroed and the session ends.
+  int rc = run_chunk(e, &token, 1, 0, nullptr, nullptr);
+  if (rc == GROUT_OK) rc = decode_common(e, token);
+  if (rc == GROUT_OK) rc = copy_logits_out(e, nullptr, nullptr);
+  const std::string first = g_last_error;
+  const int rr = grout_engine_reset(e);
+  if (rc != GROUT_OK) {
+    g_last_error = first;
+    return rc;
+  }
+  return rr;
+}
+
 int grout_engine_position(const grout_engine* e) { return e ? e->next_pos : -1; }
+
+int grout_env_flag(const char* value, int default_value) {
+  return parse_bool_or(value, default_value != 0) ? 1 : 0;
+}
 
 int grout_engine_vram_preflight(const grout_qwen3_config* c, size_t weight_bytes,
                                 size_t scratch_bytes, size_t free_bytes, size_t total_bytes,

@@ -33,14 +33,18 @@ hipError_t launch_attn_decode_split(const void* q, const void* k_cache, const vo
 // Fused decode step of one layer: QK-RMSNorm + RoPE of the new token's q
 // rows and K row, K/V cache write at d_pos[0], and split-K attention; one
 // split (nsplit == 1) writes out directly, more splits add the merge launch.
+// advance_pos (nsplit > 1 only, else ignored; may be NULL): the merge adds
+// one to *advance_pos once every split has read the position, so a captured
+// step can leave the next step's position behind.
 hipError_t launch_attn_decode_fused(const void* qkv, const void* gamma_q, const void* gamma_k,
                                     const float* rope_cos, const float* rope_sin, void* k_cache,
                                     void* v_cache, long head_stride, const uint32_t* d_pos,
                                     int max_ctx, int Hq, int Hkv, int nsplit, float eps,
                                     float qk_scale, float* part_acc, float* part_ml, void* out,
-                                    hipStream_t stream);
+                                    hipStream_t stream, uint32_t* advance_pos = nullptr);
 hipError_t launch_attn_decode_merge(const float* part_acc, const float* part_ml, void* out,
-                                    int Hq, int Hkv, int nsplit, hipStream_t stream);
+                                    int Hq, int Hkv, int nsplit, hipStream_t stream,
+                                    uint32_t* advance_pos = nullptr);
 
 hipError_t launch_fmha_prefill(const void* q, const void* k_cache, const void* v_cache,
                                void* out, int seq_len, int pos0, int Hq, int Hkv,
@@ -65,8 +69,11 @@ int argmax_num_blocks(int V);
 // 3 = f64 (through f32), round to nearest even.
 hipError_t launch_convert_to_f16(const void* src, int dtype, size_t n, void* dst,
                                  hipStream_t stream);
+// Greedy token of V f16 logits into out[0]; advance_pos (may be NULL) is
+// incremented by the same thread, for a captured decode step that leaves the
+// next step's token and position behind.
 hipError_t launch_argmax(const void* logits, float* block_max, uint32_t* block_idx, int V,
-                         uint32_t* out, hipStream_t stream);
+                         uint32_t* out, hipStream_t stream, uint32_t* advance_pos = nullptr);
 
 // Low-bit decode GEMVs (quant_gemv.hip); fmt is the ggml type id: 8 = Q8_0,
 // 12 = Q4_K, 14 = Q6_K.  Weights in the repacked layout (qweight_bytes).

@@ -618,7 +618,8 @@ __global__ __launch_bounds__(256) void argmax_blocks_kernel(const half_t* __rest
 
 __global__ __launch_bounds__(256) void argmax_reduce_kernel(const float* __restrict__ block_max,
                                                            const uint32_t* __restrict__ block_idx,
-                                                           int nblocks, uint32_t* __restrict__ out) {
+                                                           int nblocks, uint32_t* __restrict__ out,
+                                                           uint32_t* __restrict__ advance_pos) {
   __shared__ float s_m[4];
   __shared__ uint32_t s_i[4];
   float m = -3.0e38f;
@@ -633,6 +634,7 @@ __global__ __launch_bounds__(256) void argmax_reduce_kernel(const float* __restr
   if (threadIdx.x == 0) {
     for (int w = 1; w < 4; ++w) argmax_combine(m, idx, s_m[w], s_i[w]);
     out[0] = idx;
+    if (advance_pos != nullptr) advance_pos[0] += 1u;
   }
 }
 
@@ -825,10 +827,10 @@ hipError_t launch_convert_to_f16(const void* src, int dtype, size_t n, void* dst
 }
 
 hipError_t launch_argmax(const void* logits, float* block_max, uint32_t* block_idx, int V,
-                         uint32_t* out, hipStream_t stream) {
+                         uint32_t* out, hipStream_t stream, uint32_t* advance_pos) {
   const int nb = argmax_num_blocks(V);
   argmax_blocks_kernel<<<nb, 256, 0, stream>>>((const half_t*)logits, block_max, block_idx, V);
-  argmax_reduce_kernel<<<1, 256, 0, stream>>>(block_max, block_idx, nb, out);
+  argmax_reduce_kernel<<<1, 256, 0, stream>>>(block_max, block_idx, nb, out, advance_pos);
   return hipGetLastError();
 }
 

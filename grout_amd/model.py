@@ -491,13 +491,11 @@ class Engine:
         GenerationOutput::decode_graph_error (src/model.rs:1359)."""
         return (lib().grout_engine_decode_graph_error(self._h) or b"").decode()
 
-    # -- src/api.rs:162-170
+    # -- src/api.rs:153-162
     def warmup(self) -> None:
-        tok = self._meta.eos_token_ids[0] if self._meta.eos_token_ids else 0
-        tok = tok if tok < self.cfg.vocab_size else 0
-        self.prefill_greedy([tok])
-        self.decode_greedy(tok)
-        self.reset()
+        """One-token steps at positions 0 and 1 (prefill, then a decode-graph
+        replay) with the model's first stop token, then an in-place reset."""
+        call("grout_engine_warmup", self._h)
 
     def generate_greedy(self, prompt: Sequence[int], max_new_tokens: int) -> List[int]:
         """Prefill, then greedy decode: returns the max_new_tokens generated ids."""

@@ -225,13 +225,20 @@ int grout_decode_graph_create(const grout_decode_layer* layers, int num_layers,
                               int head_dim, int max_ctx, int num_splits, float eps,
                               float qk_scale, void* stream, grout_decode_graph** out);
 
-/* Uploads `position` (host-checked: position < max_ctx) into the graph's
- * device word and launches the graph on `stream`; asynchronous.
+/* Launches the graph for `position` (host-checked: position < max_ctx) on
+ * `stream`; asynchronous.  With more than one split the last layer's merge
+ * leaves position + 1 in the graph's device word, so a launch at the
+ * previous launch's position + 1 is a single hipGraphLaunch; any other
+ * position is first written into the word by a one-thread kernel.  Launches
+ * of one graph must be ordered (one stream, or ordered by the caller), as
+ * its layers share the workspace anyway.
  * Mirrors DecodeCudaGraphRunner::launch_step (src/model.rs:466-506). */
 int grout_decode_graph_launch(grout_decode_graph* graph, uint32_t position, void* stream);
 
 /* Device address of the graph's position word (u32), for callers that chain
- * their own kernels on it. */
+ * their own kernels on it: it reads `position` while the graph runs and,
+ * with more than one split, position + 1 after it.  The graph owns the word:
+ * callers only read it. */
 const uint32_t* grout_decode_graph_position_ptr(const grout_decode_graph* graph);
 
 int grout_decode_graph_destroy(grout_decode_graph* graph);

@@ -246,8 +246,8 @@ int grout_model_free(grout_model* model);
  * engine's device state on `device` and captures the decode-step graph.
  * Mirrors Engine::load (src/api.rs:60-90) minus the file loading, with the
  * graph capture of DecodeCudaGraphRunner (src/model.rs:408-596,
- * 2631-4006).  With GROUT_HIP_GRAPH_DECODE=0 in the environment, or when the
- * capture fails (a warning goes to stderr), the engine is still created and
+ * 2631-4006).  With GROUT_HIP_GRAPH_DECODE set off in the environment (0,
+ * false, off, no or empty; see grout_env_flag), or when the capture fails (a warning goes to stderr), the engine is still created and
  * decode launches the same step's kernels one by one on the engine's stream
  * (the reference's sequential fallback, src/model.rs:2130-2145, 2300-2309);
  * grout_engine_decode_graph_error says which. */
@@ -373,13 +373,30 @@ int grout_engine_vram_preflight(const grout_qwen3_config* config, size_t weight_
 int grout_engine_uses_decode_graph(const grout_engine* engine);
 
 /* Why decode runs the sequential fallback: the capture error, or the
- * GROUT_HIP_GRAPH_DECODE=0 setting; "" when the graph is in use.  Mirrors
+ * GROUT_HIP_GRAPH_DECODE setting (off); "" when the graph is in use.  Mirrors
  * GenerationOutput::decode_graph_error (src/model.rs:1359).  Valid until
  * grout_engine_destroy. */
 const char* grout_engine_decode_graph_error(const grout_engine* engine);
 
+/* Runs a dummy one-token step at positions 0 and 1 (a one-token prefill,
+ * then one decode-graph replay) with the model's first stop token (0 for
+ * an engine over caller weights), so the first request does not pay for
+ * loading library kernels or the graph's first upload; then zeroes the
+ * caches and ends the session as grout_engine_reset does (position 0, the
+ * next call must be a prefill).  Mirrors Engine::warmup (src/api.rs:153-162,
+ * api_warmup src/model.rs:2204-2212). */
+int grout_engine_warmup(grout_engine* engine);
+
 /* Position the next decode writes (number of tokens in the session). */
 int grout_engine_position(const grout_engine* engine);
+
+/* Host only.  How the engine reads a boolean switch from the environment
+ * (GROUT_HIP_GRAPH_DECODE, the counterpart of the reference's
+ * GROUT_CUDA_GRAPH_DECODE): `value` is the variable's text, NULL when unset.
+ * Returns 1 for "1", "true", "on", "yes" and 0 for "0", "false", "off", "no"
+ * or "" (whitespace trimmed, case ignored), default_value (0 or 1) for
+ * anything else or NULL.  Mirrors env_bool_or (src/model.rs:212-224). */
+int grout_env_flag(const char* value, int default_value);
 
 /* Frees everything the engine owns (not the weights).  NULL is a no-op. */
 int grout_engine_destroy(grout_engine* engine);

@@ -233,18 +233,43 @@ def test_max_ctx_cap_and_engine_queries_without_gpu():
 
 
 def test_gemv_norm_rejects_residual_aliasing_without_gpu():
-    """The norm-folded GEMV's first workgroup writes residual_out while the
-    others still read residual and x: in-place use is refused."""
+    """The norm-folded GEMVs' first workgroup writes residual_out while the
+    others still read residual and x: any overlap of those k-element f16
+    vectors is refused (same start, or an offset inside either range); a
+    range that only touches them gets past the check."""
     L = grout_amd.lib()
     keep, p = _aligned(1 << 16)
-    a = C.c_void_p(p.value + 4096)
-    b = C.c_void_p(p.value + 8192)
-    for fn in ("grout_gemv_rms_norm", "grout_gemv_rms_norm_silu_mul"):
-        f = getattr(L, fn)
-        assert f(p, a, b, p, a, p, 16, 64, 1e-6, None) == -1  # residual_out == residual
-        assert "alias" in _lib.last_error()
-        assert f(p, a, b, p, b, p, 16, 64, 1e-6, None) == -1  # residual_out == x
-        assert "alias" in _lib.last_error()
+    k = 64  # 128 bytes per vector
+    a = C.c_void_p(p.value + 4096)   # residual
+    b = C.c_void_p(p.value + 8192)   # x
+    at = lambda base, off: C.c_void_p(base.value + off)
+    overlapping = (a, b, at(a, 16), at(a, -112), at(b, 112), at(b, -16))
+    touching = (at(a, 128), at(a, -128), at(b, 128), at(b, -128))
+    f16_forms = [getattr(L, fn) for fn in ("grout_gemv_rms_norm", "grout_gemv_rms_norm_silu_mul")]
+    q_forms = [getattr(L, fn) for fn in ("grout_gemv_q_rms_norm", "grout_gemv_q_rms_norm_silu_mul")]
+    for ro in overlapping + touching:
+        calls = [lambda f=f: f(p, a, b, p, ro, p, 16, k, 1e-6, None) for f in f16_forms]
+        calls += [lambda f=f: f(8, p, a, b, p, ro, p, 16, k, 1e-6, None) for f in q_forms]
+        for c in calls:
+            rc = c()
+            if any(ro.value == o.value for o in overlapping):
+                assert rc == -1 and "overlap" in _lib.last_error(), (ro.value - p.value, rc)
+            else:
+                assert rc == 0 or "overlap" not in _lib.last_error(), ro.value - p.value
+
+
+def test_env_flag_parses_like_env_bool_or():
+    """GROUT_HIP_GRAPH_DECODE is read like the reference's env_bool_or
+    (src/model.rs:212-224): trimmed, case-insensitive, explicit spellings
+    only, anything else (or unset) the default."""
+    L = grout_amd.lib()
+    for raw in (b"1", b"true", b"TRUE", b" on ", b"Yes", b"\tyes\n"):
+        assert L.grout_env_flag(raw, 0) == 1, raw
+    for raw in (b"0", b"false", b"Off", b" no ", b"", b"   "):
+        assert L.grout_env_flag(raw, 1) == 0, raw
+    for raw in (b"2", b"enabled", b"nope", b"0x1", b"y"):
+        assert L.grout_env_flag(raw, 0) == 0 and L.grout_env_flag(raw, 1) == 1, raw
+    assert L.grout_env_flag(None, 1) == 1 and L.grout_env_flag(None, 0) == 0
 
 
 def test_low_bit_k_limit_covers_qwen3_without_gpu():

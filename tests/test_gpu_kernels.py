@@ -437,6 +437,36 @@ def test_decode_graph_replays_match_eager_ops(gpu):
             assert torch.equal(eng.k_caches[i], eager_k[i]) and torch.equal(eng.v_caches[i], eager_v[i])
             assert torch.equal(graph.attn_out[i], ref), f"layer {i} step {step}"
         torch.cuda.synchronize()
+    # Consecutive positions queued back to back with no host wait: every
+    # launch after the first finds the position word moved on by the previous
+    # replay's last merge (no write of its own), then a jump back to an
+    # earlier position is written again.
+    seq = [1200, 1201, 1202, 1203, 900]
+    qkvs = [[dev(normal(f"gqq{pos}_{i}", ((32 + 16) * D,))) for i in range(3)] for pos in seq]
+    for pos, qs in zip(seq, qkvs):
+        _say("queued graph replay", pos)
+        for i in range(3):
+            graph.qkv[i].copy_(qs[i])
+        graph.launch_step(pos)
+    import ctypes as C
+    from grout_amd._lib import lib
+
+    torch.cuda.synchronize()
+    word = C.c_uint32(0)
+    wp = lib().grout_decode_graph_position_ptr(graph._h)
+    hip = C.CDLL("libamdhip64.so")
+    assert hip.hipMemcpy(C.byref(word), C.c_void_p(wp), C.c_size_t(4), 2) == 0  # D2H
+    assert word.value == seq[-1] + 1, word.value
+    for pos, qs in zip(seq, qkvs):
+        p = torch.tensor([pos], dtype=torch.int32, device="cuda")
+        for i in range(3):
+            qr = gpu.ops.qk_norm_rope_kv_decode(qs[i], qn[i], kn[i], eng.rope, eager_k[i],
+                                                eager_v[i], p, 32)
+            ref = gpu.ops.attn_decode(qr, eager_k[i], eager_v[i], p, num_splits=graph.num_splits)
+    torch.cuda.synchronize()
+    for i in range(3):
+        assert torch.equal(eng.k_caches[i], eager_k[i]) and torch.equal(eng.v_caches[i], eager_v[i])
+    assert torch.equal(graph.attn_out[2], ref), "last queued step"
     graph.destroy()
     with pytest.raises(ValueError):
         AttentionEngine(AttentionConfig(1, 32, 8, head_dim=64), qn[:1], kn[:1])

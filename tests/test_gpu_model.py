@@ -291,7 +291,7 @@ def tiny_configs():
 
 
 @pytest.mark.parametrize("name,n_prompt,n_decode,max_ctx", [
-    ("g2", 37, 6, 64), ("g2", 1, 3, 8), ("g8", 130, 4, 512), ("4b-dims-2l", 77, 3, 4096)])
+    ("g2", 37, 6, 64), ("g2", 1, 3, 8), ("g8", 130, 4, 512), ("4b-dims-2l", 512, 3, 4096)])
 def test_engine_prefill_and_decode_vs_oracle(gpu, name, n_prompt, n_decode, max_ctx):
     cfg = tiny_configs()[name]
     print(f"engine {name} prompt={n_prompt} decode={n_decode} max_ctx={max_ctx}", flush=True)
@@ -428,6 +428,93 @@ def test_engine_sequential_decode_fallback_matches_graph(gpu, monkeypatch):
     finally:
         eng.close()
         seq.close()
+
+
+def test_engine_warmup_leaves_a_fresh_session(gpu):
+    """grout_engine_warmup (src/api.rs:153-162): one-token steps at positions 0
+    and 1, then the in-place reset: position 0, no session, and the next
+    prefill and decodes equal a fresh engine's bit for bit."""
+    from grout_amd._lib import GroutError
+
+    cfg = tiny_configs()["g2"]
+    host_w = Q.random_host_weights(cfg, seed=17, std=0.05)
+    prompt = [7, 3, 3, 250, 11, 0, 42]
+    eng = make_engine(cfg, host_w, 32)
+    fresh = make_engine(cfg, host_w, 32)
+    try:
+        eng.prefill([5, 6, 7])
+        eng.decode_greedy(8)
+        eng.warmup()
+        assert eng.position == 0
+        with pytest.raises(GroutError, match="preceding prefill"):
+            eng.decode_greedy(1)
+        a, b = eng.prefill(prompt).values, fresh.prefill(prompt).values
+        assert np.array_equal(a, b)
+        tok = int(np.argmax(a))
+        for i in range(4):
+            ta, tb = eng.decode_greedy(tok), fresh.decode_greedy(tok)
+            assert ta == tb, f"step {i}"
+            tok = ta
+        assert eng.position == fresh.position == len(prompt) + 4
+    finally:
+        eng.close()
+        fresh.close()
+
+
+def test_engine_config5_workload_graph_vs_sequential(gpu, monkeypatch):
+    """Config 5 as stated: the 36-layer Qwen3-4B engine (random N(0, 0.02)
+    fp16 weights), a seeded 512-token uniform prompt, then 256 greedy decode
+    steps.  (a) The decode-graph engine and a GROUT_HIP_GRAPH_DECODE=0
+    (sequential) engine produce the same 256 tokens and the same logits at
+    steps 0, 127 and 255, bit for bit.  (b) The decode logits at steps 0, 127 and 255 match a prefill of the
+    prompt plus the tokens decoded so far (GEMMs and the prefill FMHA against
+    the GEMVs and split-K decode, positions 512-767)."""
+    from grout_amd.model import Engine, Qwen3Config, Qwen3Weights
+
+    cfg = Qwen3Config.qwen3_4b()
+    w = Qwen3Weights.random(cfg, seed=0)
+    prompt = [int(t) for t in np.random.default_rng(512).integers(0, cfg.vocab_size, 512)]
+    probes = (0, 127, 255)
+
+    def run(eng):
+        toks, logits = [], {}
+        tok = eng.prefill_greedy(prompt)
+        for i in range(256):
+            if i in probes:
+                lg = eng.decode(tok).values
+                logits[i] = lg
+                nxt = int(np.argmax(lg))
+            else:
+                nxt = eng.decode_greedy(tok)
+            toks.append(tok)
+            tok = nxt
+        assert eng.position == 512 + 256
+        return toks, logits
+
+    eng = Engine(cfg, w, max_ctx=1024)
+    try:
+        assert eng.uses_decode_graph
+        print("config 5: graph engine, 512 + 256 steps", flush=True)
+        toks_g, logits_g = run(eng)
+        monkeypatch.setenv("GROUT_HIP_GRAPH_DECODE", "off")
+        seq = Engine(cfg, w, max_ctx=1024)
+        try:
+            assert not seq.uses_decode_graph
+            print("config 5: sequential engine, 512 + 256 steps", flush=True)
+            toks_s, logits_s = run(seq)
+        finally:
+            seq.close()
+        assert toks_g == toks_s
+        for i in probes:
+            assert np.array_equal(logits_g[i], logits_s[i]), f"step {i}"
+        print(f"config 5: {len(set(toks_g))} distinct tokens in 256 steps", flush=True)
+        for i in probes:
+            full = eng.prefill(prompt + toks_g[:i + 1]).values
+            check_logits(logits_g[i], full, f"config 5 decode step {i} vs prefill of {513 + i}")
+    finally:
+        eng.close()
+        del w
+        torch.cuda.empty_cache()
 
 
 def test_engine_vram_preflight_refuses_before_allocating(gpu):
