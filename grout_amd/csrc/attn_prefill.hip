@@ -589,10 +589,366 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
     finish(c4);
 }
 
+// Shared-stream variant: a segment is one 256-row q block, team A holding its
+// first BQ query positions and team B the next BQ (HG heads each), so both
+// teams need the same K/V tiles and consume one staged stream: team A stages
+// the K tiles and team B the V tiles (4 loads per wave per S phase instead of
+// 8), into three K and three V slots (96 KiB).  A workgroup runs the
+// complementary blocks h = nqb2-1-r and l = r back to back (their tile counts
+// add up to a constant), both teams switching from h to l at the same tile;
+// each team writes its own rows, so there is no end-of-kernel merge.  Used
+// when such pairs still give every CU a workgroup.
+//
+// Slot schedule (team B one phase behind team A; phases counted from 0):
+// G(j) = P(j).V(j) + S(j+1) = Q.K(j+1)^T runs at phase 2j+2 (A) / 2j+3 (B),
+// so K(j) is read at phases 2j and 2j+1 and V(j) at 2j+2 and 2j+3.  Team A
+// issues K(j+2) in its S phase of tile j (phase 2j+1) into the slot of
+// K(j-1), last read at phase 2j-1, and waits for it at the end of its next S
+// phase; team B issues V(j+2) at phase 2j+2 into the slot of V(j-1), last
+// read at phase 2j+1, and waits for it at the end of its next S phase (phase
+// 2j+4), four phases before its first reader.
+template <int HG>
+__global__ __launch_bounds__(512, 1) void fmha_prefill_shared_kernel(
+    const half_t* __restrict__ q, const half_t* __restrict__ k_cache,
+    const half_t* __restrict__ v_cache, half_t* __restrict__ out, int S, int pos0, int Hq,
+    int Hkv, long head_stride, float scale_log2, int nqb2) {
+  constexpr int BQ = kRowsPerTeam / HG;  // query positions per team
+  constexpr int BQ2 = 2 * BQ;           // per block
+  __shared__ __attribute__((aligned(1024))) unsigned char s_k0[kTileBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char s_k1[kTileBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char s_k2[kTileBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char s_v0[kTileBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char s_v1[kTileBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char s_v2[kTileBytes];
+
+  const int G = Hq / Hkv;
+  const int nsub = G / HG;
+  const int bid = blockIdx.x;
+  const int kvh = bid % Hkv;
+  const int rest = bid / Hkv;
+  const int hsub = rest % nsub;
+  const int r = rest / nsub;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int team = wave >> 2;
+  const int w = wave & 3;
+  const int col = lane & 15, kb = lane >> 4;
+  const int kv_len = pos0 + S;
+
+  auto tiles_of = [&](int qb) __attribute__((always_inline)) {
+    const int q_last = min(qb * BQ2 + BQ2, S) - 1;
+    return (pos0 + q_last + 1 + kBN - 1) / kBN;
+  };
+  const int h = nqb2 - 1 - r, l = r;
+  const int th = tiles_of(h), tl = l < h ? tiles_of(l) : 0;
+  const int n = th + tl;
+  auto tile_at = [&](int j) __attribute__((always_inline)) { return j < th ? j : j - th; };
+  auto qb_at = [&](int j) __attribute__((always_inline)) { return j < th ? h : l; };
+
+  const unsigned char* kh = reinterpret_cast<const unsigned char*>(k_cache + (size_t)kvh * head_stride);
+  const unsigned char* vh = reinterpret_cast<const unsigned char*>(v_cache + (size_t)kvh * head_stride);
+
+  // Row rr = 32w + 16mb + col of this team's 128 is query position
+  // qb*BQ2 + team*BQ + rr/HG of head kvh*G + hsub*HG + rr%HG.
+  auto rpos = [&](int mb) __attribute__((always_inline)) {
+    return team * BQ + (32 * w + 16 * mb + col) / HG;
+  };
+  auto rhead = [&](int mb) __attribute__((always_inline)) {
+    return kvh * G + hsub * HG + (32 * w + 16 * mb + col) % HG;
+  };
+  auto row_valid = [&](int qb, int mb) __attribute__((always_inline)) {
+    return 32 * w + 16 * mb + col < BQ * HG && qb * BQ2 + rpos(mb) < S;
+  };
+
+  half8 qf[2][4];
+  auto load_q = [&](int qb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      const bool valid = row_valid(qb, mb);
+      const half_t* qr = q + ((size_t)(qb * BQ2 + rpos(mb)) * Hq + rhead(mb)) * kHeadDim + kb * 8;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        qf[mb][c] = valid ? as_half8(load16(qr + c * 32)) : as_half8(u32x4{0u, 0u, 0u, 0u});
+    }
+  };
+
+  float m[2], lsum[2];
+  floatx4 acc[2][8];
+  auto reset_state = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      m[mb] = -1.0e30f;
+      lsum[mb] = 0.f;
+#pragma unroll
+      for (int db = 0; db < 8; ++db) acc[mb][db] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  reset_state();
+
+  // Direct-to-LDS staging of one tensor's tile by one team: wave instruction
+  // i of team wave w writes tile rows 16w + 4i .. +3 (same swizzles and
+  // source offsets as the per-team kernel).
+  const int dma0_k = (16 * w + kb) * kRowBytes + ((col ^ kb) << 4);
+  const int dma0_v = (16 * w + kb) * kRowBytes + ((col ^ (2 * kb)) << 4);
+  auto dma_tile = [&](auto is_v, const unsigned char* base, int tile, unsigned char* slot)
+                      __attribute__((always_inline)) {
+    constexpr bool V = decltype(is_v)::value;
+    const int valid_rows = kv_len - tile * kBN;  // >= 1 for every tile issued
+    __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<unsigned char*>(base) + (size_t)tile * kTileBytes, (short)0,
+        valid_rows * kRowBytes, kBufferWord3);
+    int o = V ? dma0_v : dma0_k;
+    asm volatile("" : "+v"(o));
+    lds_void* const dst = (lds_void*)(slot + 4 * w * 1024);
+    constexpr int c1 = V ? 8 : 4, c2 = V ? 1 : 8, c3 = V ? 9 : 12;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 16, o, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 16, o ^ (c1 << 4), 0, 1024, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 16, o ^ (c2 << 4), 0, 2048, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 16, o ^ (c3 << 4), 0, 3072, 0);
+  };
+  const std::true_type is_v;
+  const std::false_type is_k;
+
+  int kfrag0, vfrag0;
+  {
+    kfrag0 = col * kRowBytes + ((col >> 2) << 6) + ((kb ^ (col & 3)) << 4);
+    const int vr = 4 * kb + (col >> 2), e = col & 3, sv = swz_v(vr);
+    vfrag0 = vr * kRowBytes + ((vr & 7) << 5) + (((e >> 1) ^ (sv & 1)) << 4) + ((e & 1) << 3);
+  }
+
+  floatx4 sc[2][4];
+  half8 pf[2][2];
+
+  auto g_phase = [&](auto with_qk, const unsigned char* kread, const unsigned char* vread)
+                     __attribute__((always_inline)) {
+    constexpr bool QK = decltype(with_qk)::value;
+    __builtin_amdgcn_s_setprio(1);
+    int vbase = vfrag0, kbase = kfrag0;
+    asm volatile("" : "+v"(vbase), "+v"(kbase));
+    half8 vf[8][2];
+    half8 kf[4][4];
+    auto read_v = [&](int db) __attribute__((always_inline)) {
+      const int vo = vbase ^ (db << 5);
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc) {
+        const half4 lo = lds_read_tr16(vread + vo + 32 * cc * kRowBytes);
+        const half4 hi = lds_read_tr16(vread + vo + (32 * cc + 16) * kRowBytes);
+        vf[db][cc] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+    };
+    auto read_k = [&](int pb, int c) __attribute__((always_inline)) {
+      kf[pb][c] = as_half8(*reinterpret_cast<const u32x4*>(kread + (kbase ^ (c << 6)) + 16 * pb * kRowBytes));
+    };
+#pragma unroll
+    for (int db = 0; db < 4; ++db) read_v(db);
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        acc[mb][db] = mfma16x16x32(vf[db][0], pf[mb][0], acc[mb][db]);
+        acc[mb][db] = mfma16x16x32(vf[db][1], pf[mb][1], acc[mb][db]);
+      }
+      if (db + 4 < 8) {
+        read_v(db + 4);
+      } else if constexpr (QK) {
+        const int i = db - 4;
+        read_k(i >> 1, 2 * (i & 1));
+        read_k(i >> 1, 2 * (i & 1) + 1);
+      }
+    }
+    if constexpr (QK) {
+#pragma unroll
+      for (int pb = 0; pb < 4; ++pb) {
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+          __builtin_amdgcn_sched_barrier(0);
+          floatx4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) a = mfma16x16x32(kf[pb][c], qf[mb][c], a);
+          sc[mb][pb] = a;
+          if (pb < 2) {
+            read_k(pb + 2, 2 * mb);
+            read_k(pb + 2, 2 * mb + 1);
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(0);
+  };
+  auto qk_only = [&](const unsigned char* kread) __attribute__((always_inline)) {
+    int kbase = kfrag0;
+    asm volatile("" : "+v"(kbase));
+#pragma unroll
+    for (int pb = 0; pb < 4; ++pb) {
+      half8 kf[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        kf[c] = as_half8(*reinterpret_cast<const u32x4*>(kread + (kbase ^ (c << 6)) + 16 * pb * kRowBytes));
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        floatx4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) a = mfma16x16x32(kf[c], qf[mb][c], a);
+        sc[mb][pb] = a;
+      }
+    }
+  };
+
+  // S phase of tile j: this team's share of the staging (team A: K(j+2),
+  // team B: V(j+2); repeats of the last tile past the end go to slots that
+  // are not read again, so every S phase issues exactly 4 loads per wave),
+  // the second block's Q when tile j+1 starts it, then mask and softmax.
+  // Ends with this wave's loads of its previous S phase complete.
+  auto s_phase = [&](int j, unsigned char* kfill, unsigned char* vfill) __attribute__((always_inline)) {
+    if (j + 1 == th && tl > 0) load_q(l);
+    const int tnext = tile_at(min(j + 2, n - 1));
+    if (team == 0)
+      dma_tile(is_k, kh, tnext, kfill);
+    else
+      dma_tile(is_v, vh, tnext, vfill);
+    const int kv0 = tile_at(j) * kBN;
+    const int qrow0 = pos0 + qb_at(j) * BQ2;  // first query position of the block
+    if (kv0 + kBN - 1 > qrow0 + team * BQ) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        const int lim = qrow0 + rpos(mb) - kv0 - 4 * kb;
+#pragma unroll
+        for (int pb = 0; pb < 4; ++pb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (16 * pb + i > lim) sc[mb][pb][i] = -__builtin_inff();
+      }
+    }
+    float ts[2];
+    auto probs = [&]() __attribute__((always_inline)) {
+      const half2v ones = {(half_t)1.f, (half_t)1.f};
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        float s = 0.f;
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+          half8 p;
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              p[hh * 4 + i] = (half_t)fast_exp2(sc[mb][2 * cc + hh][i] * scale_log2 - m[mb]);
+          pf[mb][cc] = p;
+          s = __builtin_amdgcn_fdot2(__builtin_shufflevector(p, p, 0, 1), ones, s, false);
+          s = __builtin_amdgcn_fdot2(__builtin_shufflevector(p, p, 2, 3), ones, s, false);
+          s = __builtin_amdgcn_fdot2(__builtin_shufflevector(p, p, 4, 5), ones, s, false);
+          s = __builtin_amdgcn_fdot2(__builtin_shufflevector(p, p, 6, 7), ones, s, false);
+        }
+        ts[mb] = s;
+      }
+    };
+    probs();
+    if (__any(ts[0] >= kSpecLimit || ts[1] >= kSpecLimit)) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        float t = fmaxf(sc[mb][0][0], sc[mb][0][1]);
+#pragma unroll
+        for (int pb = 0; pb < 4; ++pb)
+#pragma unroll
+          for (int i = (pb == 0 ? 2 : 0); i < 4; ++i) t = fmaxf(t, sc[mb][pb][i]);
+        const float mnew = fmaxf(m[mb], col_max(t) * scale_log2);
+        const float alpha = fast_exp2(m[mb] - mnew);
+        m[mb] = mnew;
+        lsum[mb] *= alpha;
+#pragma unroll
+        for (int db = 0; db < 8; ++db) acc[mb][db] *= alpha;
+      }
+      probs();
+    }
+    lsum[0] += ts[0];
+    lsum[1] += ts[1];
+    asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  };
+
+  auto write_rows = [&](int qb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      const float lrow = col_sum(lsum[mb]);
+      if (!row_valid(qb, mb)) continue;
+      const float inv = 1.0f / lrow;
+      half_t* orow = out + ((size_t)(qb * BQ2 + rpos(mb)) * Hq + rhead(mb)) * kHeadDim;
+#pragma unroll
+      for (int db = 0; db < 8; ++db) {
+        half4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = (half_t)(acc[mb][db][i] * inv);
+        *reinterpret_cast<u32x2*>(orow + 16 * db + 4 * kb) = __builtin_bit_cast(u32x2, o);
+      }
+    }
+  };
+
+  auto g_step = [&](int j, const unsigned char* kread, const unsigned char* vread) __attribute__((always_inline)) {
+    if (j + 1 < n)
+      g_phase(std::true_type{}, kread, vread);
+    else
+      g_phase(std::false_type{}, kread, vread);
+    if (j + 1 == th && tl > 0) {
+      write_rows(h);
+      reset_state();
+    }
+  };
+
+  // ---- prologue: team A stages K(0) -> k0, K(1) -> k1, team B V(0) -> v0,
+  // V(1) -> v1; team A loads its Q now, team B after the first barrier (it
+  // idles one phase anyway) ----
+  if (team == 0) {
+    dma_tile(is_k, kh, tile_at(0), s_k0);
+    dma_tile(is_k, kh, tile_at(min(1, n - 1)), s_k1);
+    load_q(qb_at(0));
+  } else {
+    dma_tile(is_v, vh, tile_at(0), s_v0);
+    dma_tile(is_v, vh, tile_at(min(1, n - 1)), s_v1);
+  }
+  wait_vm_all();
+  lds_barrier();
+  if (team == 1) {
+    load_q(qb_at(0));
+    lds_barrier();
+  }
+  qk_only(s_k0);
+  lds_barrier();
+  // Tile j: G reads K slot (j+1)%3 and V slot j%3; S stages into slot
+  // (j+2)%3.  Three tiles per trip keep every slot a compile-time constant.
+  for (int j = 0; j < n; j += 3) {
+    s_phase(j, s_k2, s_v2);
+    lds_barrier();
+    g_step(j, s_k1, s_v0);
+    lds_barrier();
+    if (j + 1 < n) {
+      s_phase(j + 1, s_k0, s_v0);
+      lds_barrier();
+      g_step(j + 1, s_k2, s_v1);
+      lds_barrier();
+      if (j + 2 < n) {
+        s_phase(j + 2, s_k1, s_v1);
+        lds_barrier();
+        g_step(j + 2, s_k0, s_v2);
+        lds_barrier();
+      }
+    }
+  }
+  if (team == 0) lds_barrier();  // team B runs one phase more
+  // Loads of the last S phases may still target LDS: drain before exiting.
+  wait_vm_all();
+  write_rows(tl > 0 ? l : h);
+}
+
 // GROUT_FMHA_PREFILL_PAIRED=0/1 forces the single-block / paired work split
-// (tests exercise both); by default pairs are used when they fill the GPU.
-static int prefill_paired_override() {
-  const char* e = std::getenv("GROUT_FMHA_PREFILL_PAIRED");
+// of the per-team kernel, GROUT_FMHA_PREFILL_SHARED=0/1 the per-team /
+// shared-stream kernel (tests exercise every form); by default the shared
+// stream is used when its block pairs fill the GPU, else per-team pairs when
+// they do, else single blocks.
+static int env_override(const char* name) {
+  const char* e = std::getenv(name);
   return e ? std::atoi(e) : -1;
 }
 
@@ -609,15 +965,25 @@ hipError_t launch_fmha_prefill(const void* q, const void* k_cache, const void* v
   // Complementary pairs give every workgroup the same work; they are used
   // when there are enough of them for one workgroup per CU (256 CUs).
   const long pair_blocks = (long)((nqb + 1) / 2) * per_block;
+  // shared stream: 256-row blocks of 2*BQ positions, complementary pairs
+  const int nqb2 = (seq_len + 2 * BQ - 1) / (2 * BQ);
+  const long shared_blocks = (long)((nqb2 + 1) / 2) * per_block;
+  int shared = shared_blocks >= 256 ? 1 : 0;
+  if (const int o = env_override("GROUT_FMHA_PREFILL_SHARED"); o == 0 || o == 1) shared = o;
   int paired = pair_blocks >= 256 ? 1 : 0;
-  if (const int o = prefill_paired_override(); o == 0 || o == 1) paired = o;
-  const long blocks = (paired ? (nqb + 1) / 2 : nqb) * (long)per_block;
+  if (const int o = env_override("GROUT_FMHA_PREFILL_PAIRED"); o == 0 || o == 1) paired = o;
+  const long blocks = shared ? shared_blocks : (paired ? (nqb + 1) / 2 : nqb) * (long)per_block;
   if (blocks <= 0 || blocks > 0x7fffffffL) return hipErrorInvalidValue;
-#define GROUT_PREFILL_CASE(hg)                                                            \
-  case hg:                                                                                \
-    fmha_prefill_kernel<hg><<<(unsigned)blocks, 512, 0, stream>>>(                        \
-        (const half_t*)q, (const half_t*)k_cache, (const half_t*)v_cache, (half_t*)out,   \
-        seq_len, pos0, Hq, Hkv, head_stride, scale_log2, nqb, paired);                    \
+#define GROUT_PREFILL_CASE(hg)                                                             \
+  case hg:                                                                                 \
+    if (shared)                                                                            \
+      fmha_prefill_shared_kernel<hg><<<(unsigned)blocks, 512, 0, stream>>>(                \
+          (const half_t*)q, (const half_t*)k_cache, (const half_t*)v_cache, (half_t*)out,  \
+          seq_len, pos0, Hq, Hkv, head_stride, scale_log2, nqb2);                          \
+    else                                                                                   \
+      fmha_prefill_kernel<hg><<<(unsigned)blocks, 512, 0, stream>>>(                       \
+          (const half_t*)q, (const half_t*)k_cache, (const half_t*)v_cache, (half_t*)out,  \
+          seq_len, pos0, Hq, Hkv, head_stride, scale_log2, nqb, paired);                   \
     break;
   switch (HG) {
     GROUT_PREFILL_CASE(1)
