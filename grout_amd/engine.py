@@ -125,7 +125,9 @@ class DecodeGraph:
         self._h = handle
 
     def launch_step(self, position: int) -> None:
-        """Upload `position` and replay the graph on the current stream (async)."""
+        """Replay the graph for `position` on the current stream (async); a
+        position one past the previous launch's needs no upload (the graph's
+        last merge leaves it in the position word)."""
         if self._h is None:
             raise RuntimeError("decode graph destroyed")
         call("grout_decode_graph_launch", self._h, position,

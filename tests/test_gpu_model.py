@@ -708,10 +708,15 @@ def test_engine_load_matches_oracle(gpu, tmp_path):
         tol = check_logits(got, ref, "loaded prefill")
         tok = int(np.argmax(got))
         check_token(tok, ref, tol, "loaded prefill token")
+        first = eng.prefill(prompt).values
         for i in range(3):
             got = eng.decode(tok).values
             ref, _ = orc.decode(tok, nthreads=8)
             check_logits(got, ref, f"loaded decode {i}")
             tok = int(np.argmax(got))
+        # warmup with the checkpoint's first stop token (7), then a fresh session
+        eng.warmup()
+        assert eng.position == 0
+        assert np.array_equal(eng.prefill(prompt).values, first)
     finally:
         eng.close()
