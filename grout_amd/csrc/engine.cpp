@@ -792,8 +792,10 @@ static int check_gemv_norm(const void* W, const void* residual, const void* x,
   GROUT_NEED(n >= 1, GROUT_EINVAL, "n=%d", n);
   GROUT_CHECK(check_norm(1, k, eps));
   GROUT_CHECK(check_ptrs16({{W, "W"}, {x, "x"}, {gamma, "gamma"}}));
-  if (residual) GROUT_CHECK(check_ptrs16({{residual, "residual"}, {residual_out, "residual_out"}}));
-  GROUT_CHECK(check_residual_out(residual, x, residual_out, k));
+  if (residual) {  // residual_out is written only with a residual
+    GROUT_CHECK(check_ptrs16({{residual, "residual"}, {residual_out, "residual_out"}}));
+    GROUT_CHECK(check_residual_out(residual, x, residual_out, k));
+  }
   GROUT_NEED(y != nullptr && (reinterpret_cast<uintptr_t>(y) & 1u) == 0, GROUT_EALIGN,
              "y is NULL or not 2-byte aligned");
   return GROUT_OK;
