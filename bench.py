@@ -265,6 +265,10 @@ def bench_decode_graph(grout_amd, Hq, Hkv, ctx, max_ctx, n_layers, steps, warmup
     return ms
 
 
+PREFILL_US_SOURCE = ("HIP events around one graph replay of the timed calls; us_dist spreads "
+                     "20 replays of 100 calls, each replay's average carrying its ~6.5 us start gap")
+
+
 def bench_prefill(ops, S, Hq, Hkv, steps, warmup):
     import torch
 
@@ -277,7 +281,7 @@ def bench_prefill(ops, S, Hq, Hkv, steps, warmup):
     call = lambda i=0: ops.fmha_prefill(q, kc, vc, 0, out=out)
     ms = time_launches(call, steps, warmup, torch.cuda.current_stream(dev))
     flop = 4.0 * Hq * D * S * (S + 1) / 2
-    return dict(ms=ms, flop=flop, dist=time_distribution(call, calls=20),
+    return dict(ms=ms, flop=flop, dist=time_distribution(call, calls=100),
                 library=bench_prefill_library(q, kc, vc, out, steps, warmup))
 
 
@@ -844,7 +848,7 @@ def main():
         line["prefill"] = {"workload": "qwen3-4b causal prefill FMHA S=2048 Hq=32 Hkv=8 D=128",
                            "us": round(r["ms"] * 1e3, 2), "tflops": round(tf, 1),
                            "mfma_frac": round(tf / F16_MFMA_PEAK_TFLOPS, 4),
-                           "flop": r["flop"], "us_dist": r["dist"]}
+                           "flop": r["flop"], "us_source": PREFILL_US_SOURCE, "us_dist": r["dist"]}
         sweep = {}
         for S, rr in res["prefill_sweep"].items():
             t = rr["flop"] / (rr["ms"] * 1e-3) / 1e12
