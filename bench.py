@@ -36,7 +36,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--only", default="",
-                    help="comma list: decode32b,prefill,decode4b,norm,engine4b,engine4b_q4km (gemv, qgemv, "
+                    help="comma list: decode32b,prefill,decode4b,shard,norm,engine4b,engine4b_q4km (gemv, qgemv, "
                          "engine4b_q5km: only when named)")
     ap.add_argument("--eager", action="store_true",
                     help="launch the timed calls from the host instead of replaying a captured "
@@ -237,6 +237,38 @@ def bench_decode32b_sweep(ops, ctxs, steps, warmup, sweep_steps=100):
               flush=True)
     b.close()
     return out
+
+
+SHARD_KV_SPLITS = (32, 64, 128, 256)
+
+
+def bench_shard(ops, steps, warmup, sweep_steps=100):
+    """One GPU's share of a Qwen3-32B decode layer at 32k sharded over 8 GPUs,
+    at its real shape (multi-GPU runs are outside this build).  kv-head
+    sharding: each GPU holds one kv head and its 8 query heads (Hkv=1, Hq=8,
+    ctx 32768, 24 rotating layer caches > the Infinity Cache), split count
+    swept as for config 4.  Sequence sharding over 4 GPUs: each GPU runs the
+    8192-position slice (the decode32b_sweep entry at ctx 8192, 32 splits)
+    and, after the all-gather, the merge of 4 x 8 gathered partials, timed
+    here alone."""
+    import torch
+
+    b = DecodeBench(8, 1, 32768, 24)
+    ctx = 32768
+    sweep = {ns: b.time_step(ctx, ns, sweep_steps, warmup) for ns in SHARD_KV_SPLITS}
+    best = min(sweep, key=sweep.get)
+    kv = dict(step_ms=b.time_step(ctx, best, steps, warmup),
+              split_ms=b.time_split(ctx, best, steps, warmup), alg_bytes=b.alg_bytes(ctx),
+              num_splits=best, sweep_us={ns: round(ms * 1e3, 2) for ns, ms in sweep.items()})
+    b.close()
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(3)
+    acc = torch.randn((8, 32, 8, D), generator=g, device=dev, dtype=torch.float32)
+    ml = torch.stack([torch.randn((8, 32, 8), generator=g, device=dev),
+                      torch.rand((8, 32, 8), generator=g, device=dev) + 1.0], -1)
+    out = torch.empty((64, D), dtype=torch.float16, device=dev)
+    merge_ms = time_launches(lambda i=0: ops.splitk_reduce_merge(acc, ml, out=out), steps, warmup)
+    return dict(kv_head=kv, merge_ms=merge_ms)
 
 
 def bench_decode_graph(grout_amd, Hq, Hkv, ctx, max_ctx, n_layers, steps, warmup):
@@ -773,6 +805,9 @@ def main():
             return r
         res["decode4b"] = guarded(decode4b)
         print(f"# decode4b {res['decode4b']}", file=sys.stderr, flush=True)
+    if want("shard"):
+        res["shard"] = guarded(lambda: bench_shard(ops, a.steps, a.warmup))
+        print(f"# shard {res['shard']}", file=sys.stderr, flush=True)
     if want("norm"):
         res["norm"] = guarded(lambda: bench_norm(ops, 2048, 32, 8, 32768, a.steps, a.warmup))
         print(f"# norm {res['norm']}", file=sys.stderr, flush=True)
@@ -871,6 +906,26 @@ def main():
                             "us_per_layer": round(r["step_ms"] * 1e3, 2), "gbs": round(gbs, 1),
                             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "num_splits": r["num_splits"],
                             "graph_36_layers_us": round(r["graph_ms"] * 1e3, 1)}
+    if ok("shard"):
+        r = res["shard"]
+        kv = r["kv_head"]
+        gbs = kv["alg_bytes"] / (kv["step_ms"] * 1e-3) / 1e9
+        sgbs = kv["alg_bytes"] / (kv["split_ms"] * 1e-3) / 1e9
+        seq = line.get("decode32b_sweep", {}).get("8192", {})
+        line["shard"] = {
+            "workload": "one GPU's share of a qwen3-32b decode layer at ctx 32768 sharded over "
+                        "GPUs (design only: no multi-GPU run in this build)",
+            "kv_head_8way": {"shape": "Hq=8 Hkv=1 ctx 32768, 24 layer caches",
+                             "num_splits": kv["num_splits"],
+                             "step_us": round(kv["step_ms"] * 1e3, 2),
+                             "step_gbs": round(gbs, 1), "step_hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                             "split_us": round(kv["split_ms"] * 1e3, 2),
+                             "split_hbm_frac": round(sgbs / HBM_PEAK_GBS, 4),
+                             "splits_swept_us": kv["sweep_us"]},
+            "sequence_4way": {"slice": "Hq=64 Hkv=8, 8192 positions per GPU, 32 splits: the "
+                                       "decode32b_sweep entry at ctx 8192",
+                              "slice_split_us": seq.get("split_us"),
+                              "merge_of_4x8_gathered_partials_us": round(r["merge_ms"] * 1e3, 2)}}
     if ok("norm"):
         r = res["norm"]
         gbs = r["alg_bytes"] / (r["ms"] * 1e-3) / 1e9

@@ -234,6 +234,56 @@ def test_decode_split_then_merge_matches_fused_call(gpu):
     assert np.allclose(L.numpy(), ref_L, rtol=2e-3)
 
 
+def test_sharded_decode_layer_matches_the_whole_layer(gpu):
+    """The two ways one Qwen3-32B decode layer at 32k would be spread over
+    GPUs, run as each GPU's share on this one: (1) by kv head, one kv head and
+    its 8 q heads per GPU (Hkv=1 slices of the cache); (2) by sequence, each
+    GPU running the split pass on its slice of the context and the slices'
+    partials gathered ([Hkv][P x splits][G][...], what an all-gather delivers)
+    into one merge.  Each result is checked against the oracle on the whole
+    layer and against the unsharded call."""
+    from grout_amd._lib import call
+
+    Hq, Hkv, max_ctx = 64, 8, 32768
+    G = Hq // Hkv
+    ctx = max_ctx
+    _say("sharded decode", Hq, Hkv, ctx)
+    q = normal("shq", (Hq, D))
+    kc, vc = normal("shk", (Hkv, max_ctx, D)), normal("shv", (Hkv, max_ctx, D))
+    ref = O.attention_decode(q, kc, vc, ctx - 1, nthreads=8)
+    qd, kd, vd = dev(q), dev(kc), dev(vc)
+    p = torch.tensor([ctx - 1], dtype=torch.int32, device="cuda")
+    whole = gpu.ops.attn_decode(qd, kd, vd, p, num_splits=32)
+    # (1) kv-head shards
+    by_head = torch.cat([gpu.ops.attn_decode(qd[h * G:(h + 1) * G], kd[h:h + 1], vd[h:h + 1], p,
+                                             num_splits=32) for h in range(Hkv)])
+    # (2) sequence shards: 4 aligned slices x 8 splits, and 3 ragged slices
+    def by_sequence(bounds, ns):
+        accs, mls = [], []
+        for a, b in zip(bounds[:-1], bounds[1:]):
+            acc = torch.empty((Hkv, ns, G, D), dtype=torch.float32, device="cuda")
+            ml = torch.empty((Hkv, ns, G, 2), dtype=torch.float32, device="cuda")
+            pl = torch.tensor([b - a - 1], dtype=torch.int32, device="cuda")
+            call("grout_fmha_decode_gqa_split", qd.data_ptr(), kd.data_ptr() + a * D * 2,
+                 vd.data_ptr() + a * D * 2, acc.data_ptr(), ml.data_ptr(), pl.data_ptr(), Hq, Hkv,
+                 D, b - a, max_ctx * D, ns, D ** -0.5, torch.cuda.current_stream().cuda_stream)
+            accs.append(acc)
+            mls.append(ml)
+            torch.cuda.synchronize()  # pl lives until the pass has read it
+        return gpu.ops.splitk_reduce_merge(torch.cat(accs, 1).contiguous(),
+                                           torch.cat(mls, 1).contiguous())
+    by_seq4 = by_sequence([0, 8192, 16384, 24576, 32768], 8)
+    by_seq3 = by_sequence([0, 10000, 22000, 32768], 8)
+    torch.cuda.synchronize()
+    w = host_f32(whole)
+    for name, out in (("kv-head shards", by_head), ("4 sequence shards", by_seq4),
+                      ("3 ragged sequence shards", by_seq3)):
+        got = host_f32(out)
+        assert_close(got, ref, f"{name} vs oracle")
+        # same math, other accumulation orders: within a few f16 ulps of the whole call
+        assert np.abs(got - w).max() <= 4 * 2.0 ** -11 * max(1.0, np.abs(w).max()), name
+
+
 def test_decode_reuses_workspace_across_calls(gpu):
     """Consecutive decodes on one workspace (as the decode graph does)."""
     Hq, Hkv, max_ctx, ns = 64, 8, 4096, 24
