@@ -12,7 +12,10 @@
 //  * a team of 4 waves owns a q block of 128 query rows = BQ query positions
 //    x HG heads of one kv group (HG = the largest divisor of G that is <= 8,
 //    BQ = floor(128/HG)), so every K/V tile staged in LDS serves HG heads;
-//    each wave owns 32 rows (two 16-column MFMA blocks);
+//    each wave owns 32 rows (two 16-column MFMA blocks).  Short prompts,
+//    whose 128-row blocks cannot give every CU a workgroup, use 64-row
+//    blocks instead (16 rows per wave: twice the workgroups, each with half
+//    the MFMA work per tile);
 //  * the workgroup holds two teams, A = waves 0-3 and B = waves 4-7, one wave
 //    of each per SIMD.  Per kv tile a team runs two phases: G (the MFMA work:
 //    P(j).V(j) and S(j+1) = Q.K(j+1)^T) and S (the VALU work: mask, row max,
@@ -115,12 +118,15 @@ __device__ __forceinline__ float col_sum(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-template <int HG>
+// MB: 16-row MFMA blocks per wave (2: 32 rows per wave, 128 per team; 1: 16
+// and 64, for short prompts, where the 128-row form leaves CUs idle).
+template <int HG, int MB>
 __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
     const half_t* __restrict__ q, const half_t* __restrict__ k_cache,
     const half_t* __restrict__ v_cache, half_t* __restrict__ out, int S, int pos0, int Hq,
     int Hkv, long head_stride, float scale_log2, int nqb, int paired) {
-  constexpr int BQ = kRowsPerTeam / HG;
+  constexpr int RT = 64 * MB;  // rows per team
+  constexpr int BQ = RT / HG;
   // Per team: two K slots and two V slots, each slot its own LDS object, so
   // the compiler knows that the loads filling one slot do not alias the
   // fragment reads of another and keeps them in flight.
@@ -185,18 +191,18 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
 
   // Row rr = 32w + 16mb + col of a q block is query position qb*BQ + rr/HG of
   // head kvh*G + hsub*HG + rr%HG.
-  auto rpos = [&](int mb) __attribute__((always_inline)) { return (32 * w + 16 * mb + col) / HG; };
+  auto rpos = [&](int mb) __attribute__((always_inline)) { return (16 * MB * w + 16 * mb + col) / HG; };
   auto rhead = [&](int mb) __attribute__((always_inline)) {
-    return kvh * G + hsub * HG + (32 * w + 16 * mb + col) % HG;
+    return kvh * G + hsub * HG + (16 * MB * w + 16 * mb + col) % HG;
   };
   auto row_valid = [&](int qb, int mb) __attribute__((always_inline)) {
-    return 32 * w + 16 * mb + col < BQ * HG && qb * BQ + rpos(mb) < S;
+    return 16 * MB * w + 16 * mb + col < BQ * HG && qb * BQ + rpos(mb) < S;
   };
 
-  half8 qf[2][4];
+  half8 qf[MB][4];
   auto load_q = [&](int qb) __attribute__((always_inline)) {
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
+    for (int mb = 0; mb < MB; ++mb) {
       const bool valid = row_valid(qb, mb);
       const half_t* qr = q + ((size_t)(qb * BQ + rpos(mb)) * Hq + rhead(mb)) * kHeadDim + kb * 8;
 #pragma unroll
@@ -209,11 +215,11 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
   // sum of p (the lane group kb covers 16 of every 64 positions); acc: O^T
   // fragments.  m starts finite and masked scores are -inf, so a row whose
   // tiles so far are all masked keeps p = 0 (exp2(-inf)) instead of exp2(0).
-  float m[2], lsum[2];
-  floatx4 acc[2][8];
+  float m[MB], lsum[MB];
+  floatx4 acc[MB][8];
   auto reset_state = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
+    for (int mb = 0; mb < MB; ++mb) {
       m[mb] = -1.0e30f;
       lsum[mb] = 0.f;
 #pragma unroll
@@ -270,8 +276,8 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
              ((e & 1) << 3);
   }
 
-  floatx4 sc[2][4];   // S^T(j+1): element (pb, i) is kv position kv0 + 16pb + 4kb + i
-  half8 pf[2][2];     // P(j) as the B operand of P.V (positions 32cc + {4kb.., 16+4kb..})
+  floatx4 sc[MB][4];   // S^T(j+1): element (pb, i) is kv position kv0 + 16pb + 4kb + i
+  half8 pf[MB][2];     // P(j) as the B operand of P.V (positions 32cc + {4kb.., 16+4kb..})
 
   // S(j+1) = K(j+1).Q^T (each K fragment serves both 16-row blocks).
   auto qk = [&](const unsigned char* kread, int kbase) __attribute__((always_inline)) {
@@ -282,7 +288,7 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
       for (int c = 0; c < 4; ++c)
         kf[c] = as_half8(*reinterpret_cast<const u32x4*>(kread + (kbase ^ (c << 6)) + 16 * pb * kRowBytes));
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
+      for (int mb = 0; mb < MB; ++mb) {
         floatx4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int c = 0; c < 4; ++c) s = mfma16x16x32(kf[c], qf[mb][c], s);
@@ -326,7 +332,7 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
     for (int db = 0; db < 8; ++db) {
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
+      for (int mb = 0; mb < MB; ++mb) {
         acc[mb][db] = mfma16x16x32(vf[db][0], pf[mb][0], acc[mb][db]);
         acc[mb][db] = mfma16x16x32(vf[db][1], pf[mb][1], acc[mb][db]);
       }
@@ -342,15 +348,20 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
 #pragma unroll
       for (int pb = 0; pb < 4; ++pb) {
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
+        for (int mb = 0; mb < MB; ++mb) {
           __builtin_amdgcn_sched_barrier(0);
           floatx4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int c = 0; c < 4; ++c) a = mfma16x16x32(kf[pb][c], qf[mb][c], a);
           sc[mb][pb] = a;
           if (pb < 2) {
-            read_k(pb + 2, 2 * mb);
-            read_k(pb + 2, 2 * mb + 1);
+            if constexpr (MB == 2) {
+              read_k(pb + 2, 2 * mb);
+              read_k(pb + 2, 2 * mb + 1);
+            } else {
+#pragma unroll
+              for (int c = 0; c < 4; ++c) read_k(pb + 2, c);
+            }
           }
         }
       }
@@ -383,7 +394,7 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
     const int qrow0 = pos0 + qb_at(j) * BQ;  // first query position of the block
     if (kv0 + kBN - 1 > qrow0) {
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
+      for (int mb = 0; mb < MB; ++mb) {
         // element (pb, i) is kv position kv0 + 4kb + 16pb + i: compare the
         // immediate 16pb + i against one per-lane limit
         const int lim = qrow0 + rpos(mb) - kv0 - 4 * kb;
@@ -399,11 +410,11 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
     // (a score at least ~8 above m, an overflow to inf, or m still at its
     // initial -1e30) sends the wave to the exact path: tile row max, rescale
     // of what was accumulated, P again.  Accepted tiles keep p <= 2^8.
-    float ts[2];
+    float ts[MB];
     auto probs = [&]() __attribute__((always_inline)) {
       const half2v ones = {(half_t)1.f, (half_t)1.f};
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
+      for (int mb = 0; mb < MB; ++mb) {
         float s = 0.f;
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
@@ -423,9 +434,12 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
       }
     };
     probs();
-    if (__any(ts[0] >= kSpecLimit || ts[1] >= kSpecLimit)) {
+    bool over = false;
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
+    for (int mb = 0; mb < MB; ++mb) over = over || ts[mb] >= kSpecLimit;
+    if (__any(over)) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
         float t = fmaxf(sc[mb][0][0], sc[mb][0][1]);
 #pragma unroll
         for (int pb = 0; pb < 4; ++pb)
@@ -440,8 +454,8 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
       }
       probs();
     }
-    lsum[0] += ts[0];
-    lsum[1] += ts[1];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) lsum[mb] += ts[mb];
     wait_vm_keep8();
   };
 
@@ -449,11 +463,11 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
   const std::integral_constant<int, 4> c4;
   const std::integral_constant<int, 8> c8;
   // Output rows of block qb, d blocks [DB0, DB0 + NDB).
-  auto write_rows = [&](auto db0_c, auto ndb_c, int qb, const float (&lrow)[2])
+  auto write_rows = [&](auto db0_c, auto ndb_c, int qb, const float (&lrow)[MB])
                         __attribute__((always_inline)) {
     constexpr int DB0 = decltype(db0_c)::value, NDB = decltype(ndb_c)::value;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
+    for (int mb = 0; mb < MB; ++mb) {
       if (!row_valid(qb, mb)) continue;
       const float inv = 1.0f / lrow[mb];
       half_t* orow = out + ((size_t)(qb * BQ + rpos(mb)) * Hq + rhead(mb)) * kHeadDim;
@@ -466,9 +480,9 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
       }
     }
   };
-  auto row_sums = [&](float (&lrow)[2]) __attribute__((always_inline)) {
+  auto row_sums = [&](float (&lrow)[MB]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) lrow[mb] = col_sum(lsum[mb]);
+    for (int mb = 0; mb < MB; ++mb) lrow[mb] = col_sum(lsum[mb]);
   };
 
   // G phase of tile j plus, after the last tile of the first segment when a
@@ -479,7 +493,7 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
     else
       g_phase(std::false_type{}, kread, vread);
     if (j + 1 == n0 && n1 > 0) {
-      float lrow[2];
+      float lrow[MB];
       row_sums(lrow);
       write_rows(c0, c8, qb0, lrow);
       reset_state();
@@ -531,7 +545,7 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
   wait_vm_all();
   lds_barrier();
 
-  float lrow[2];
+  float lrow[MB];
   row_sums(lrow);
   if (!merge_h) {
     if (n > 0) write_rows(c0, c8, n1 > 0 ? qb1 : qb0, lrow);
@@ -550,7 +564,7 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
   auto xchg = [&](auto give_c) __attribute__((always_inline)) {
     constexpr int GIVE = decltype(give_c)::value;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+    for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         *reinterpret_cast<floatx4*>(accbuf + team * 8192 + ((mb * 4 + i) * 64 + lane) * 16) =
@@ -560,13 +574,13 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
     xchg(c4);
   else
     xchg(c0);
-  *reinterpret_cast<floatx4*>(mlbuf + team * 1024) = floatx4{m[0], m[1], lrow[0], lrow[1]};
+  *reinterpret_cast<floatx4*>(mlbuf + team * 1024) = floatx4{m[0], m[MB - 1], lrow[0], lrow[MB - 1]};
   lds_barrier();
   const floatx4 mlo = *reinterpret_cast<const floatx4*>(mlbuf + other * 1024);
   auto finish = [&](auto keep_c) __attribute__((always_inline)) {
     constexpr int KEEP = decltype(keep_c)::value;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
+    for (int mb = 0; mb < MB; ++mb) {
       const float ma = team == 0 ? m[mb] : mlo[mb], mbb = team == 0 ? mlo[mb] : m[mb];
       const float la = team == 0 ? lrow[mb] : mlo[2 + mb], lb = team == 0 ? mlo[2 + mb] : lrow[mb];
       const float mn = fmaxf(ma, mbb);
@@ -943,10 +957,12 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_shared_kernel(
 }
 
 // GROUT_FMHA_PREFILL_PAIRED=0/1 forces the single-block / paired work split
-// of the per-team kernel, GROUT_FMHA_PREFILL_SHARED=0/1 the per-team /
-// shared-stream kernel (tests exercise every form); by default the shared
-// stream is used when its block pairs fill the GPU, else per-team pairs when
-// they do, else single blocks.
+// of the per-team kernel, GROUT_FMHA_PREFILL_WAVE_ROWS=16/32 its 64-row /
+// 128-row blocks, GROUT_FMHA_PREFILL_SHARED=0/1 the per-team / shared-stream
+// kernel (tests exercise every form).  By default the shared stream is used
+// when its block pairs fill the GPU (one workgroup per CU, 256 CUs), else the
+// per-team kernel with 128-row blocks when their pairs fill it, else with
+// 64-row blocks, paired when those pairs fill it, else single blocks.
 static int env_override(const char* name) {
   const char* e = std::getenv(name);
   return e ? std::atoi(e) : -1;
@@ -970,9 +986,17 @@ hipError_t launch_fmha_prefill(const void* q, const void* k_cache, const void* v
   const long shared_blocks = (long)((nqb2 + 1) / 2) * per_block;
   int shared = shared_blocks >= 256 ? 1 : 0;
   if (const int o = env_override("GROUT_FMHA_PREFILL_SHARED"); o == 0 || o == 1) shared = o;
-  int paired = pair_blocks >= 256 ? 1 : 0;
+  // 64-row blocks (16 rows per wave) when 128-row pairs would leave CUs idle
+  int wave_rows = pair_blocks >= 256 ? 32 : 16;
+  if (const int o = env_override("GROUT_FMHA_PREFILL_WAVE_ROWS"); o == 16 || o == 32)
+    wave_rows = o;
+  const int BQr = wave_rows == 32 ? BQ : (kRowsPerTeam / 2) / HG;
+  const int nqbr = (seq_len + BQr - 1) / BQr;
+  const long pair_blocks_r = (long)((nqbr + 1) / 2) * per_block;
+  int paired = pair_blocks_r >= 256 ? 1 : 0;
   if (const int o = env_override("GROUT_FMHA_PREFILL_PAIRED"); o == 0 || o == 1) paired = o;
-  const long blocks = shared ? shared_blocks : (paired ? (nqb + 1) / 2 : nqb) * (long)per_block;
+  const long blocks =
+      shared ? shared_blocks : (paired ? (nqbr + 1) / 2 : nqbr) * (long)per_block;
   if (blocks <= 0 || blocks > 0x7fffffffL) return hipErrorInvalidValue;
 #define GROUT_PREFILL_CASE(hg)                                                             \
   case hg:                                                                                 \
@@ -980,10 +1004,14 @@ hipError_t launch_fmha_prefill(const void* q, const void* k_cache, const void* v
       fmha_prefill_shared_kernel<hg><<<(unsigned)blocks, 512, 0, stream>>>(                \
           (const half_t*)q, (const half_t*)k_cache, (const half_t*)v_cache, (half_t*)out,  \
           seq_len, pos0, Hq, Hkv, head_stride, scale_log2, nqb2);                          \
-    else                                                                                   \
-      fmha_prefill_kernel<hg><<<(unsigned)blocks, 512, 0, stream>>>(                       \
+    else if (wave_rows == 32)                                                              \
+      fmha_prefill_kernel<hg, 2><<<(unsigned)blocks, 512, 0, stream>>>(                    \
           (const half_t*)q, (const half_t*)k_cache, (const half_t*)v_cache, (half_t*)out,  \
-          seq_len, pos0, Hq, Hkv, head_stride, scale_log2, nqb, paired);                   \
+          seq_len, pos0, Hq, Hkv, head_stride, scale_log2, nqbr, paired);                  \
+    else                                                                                   \
+      fmha_prefill_kernel<hg, 1><<<(unsigned)blocks, 512, 0, stream>>>(                    \
+          (const half_t*)q, (const half_t*)k_cache, (const half_t*)v_cache, (half_t*)out,  \
+          seq_len, pos0, Hq, Hkv, head_stride, scale_log2, nqbr, paired);                  \
     break;
   switch (HG) {
     GROUT_PREFILL_CASE(1)

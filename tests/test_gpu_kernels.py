@@ -331,12 +331,16 @@ def _random_prefill_cases(n=10, seed=4048):
     return cases
 
 
-@pytest.mark.parametrize("shared", ["default", "1"])
+@pytest.mark.parametrize("form", ["default", "rows32", "shared"])
 @pytest.mark.parametrize("S,Hq,Hkv,pos0", _random_prefill_cases())
-def test_prefill_random_shapes_vs_oracle(gpu, monkeypatch, shared, S, Hq, Hkv, pos0):
-    if shared != "default":
-        monkeypatch.setenv("GROUT_FMHA_PREFILL_SHARED", shared)
-    _say("prefill random", shared, S, Hq, Hkv, pos0)
+def test_prefill_random_shapes_vs_oracle(gpu, monkeypatch, form, S, Hq, Hkv, pos0):
+    """Default work split (64-row blocks at these lengths), 128-row blocks
+    forced, and the shared K/V stream forced."""
+    if form == "rows32":
+        monkeypatch.setenv("GROUT_FMHA_PREFILL_WAVE_ROWS", "32")
+    if form == "shared":
+        monkeypatch.setenv("GROUT_FMHA_PREFILL_SHARED", "1")
+    _say("prefill random", form, S, Hq, Hkv, pos0)
     max_ctx = pos0 + S + 3
     q = normal(f"rpq{S}_{Hq}", (S, Hq, D))
     kc, vc = normal(f"rpk{S}_{Hkv}", (Hkv, max_ctx, D)), normal(f"rpv{S}_{Hkv}", (Hkv, max_ctx, D))
@@ -346,22 +350,25 @@ def test_prefill_random_shapes_vs_oracle(gpu, monkeypatch, shared, S, Hq, Hkv, p
     assert_close(host_f32(out), ref, f"prefill S={S} Hq={Hq} Hkv={Hkv} pos0={pos0}")
 
 
-@pytest.mark.parametrize("mode", ["single", "paired", "shared"])
+@pytest.mark.parametrize("mode", ["single", "paired", "single64", "paired64", "shared"])
 @pytest.mark.parametrize("S,Hq,Hkv,pos0", [
     (1, 32, 8, 0), (17, 32, 8, 0), (130, 64, 8, 0), (200, 32, 8, 77), (77, 40, 8, 9),
     (33, 16, 1, 0), (700, 32, 8, 100), (1000, 16, 4, 0), (2048, 24, 8, 0), (600, 56, 8, 7),
     (3000, 32, 8, 0), (523, 8, 8, 300)])
 def test_prefill_work_splits_vs_oracle(gpu, monkeypatch, mode, S, Hq, Hkv, pos0):
     """Every work split of the prefill FMHA, forced through
-    GROUT_FMHA_PREFILL_SHARED / _PAIRED: per-team K/V staging with one q block
-    per workgroup (its tiles split over the two 4-wave teams) or complementary
-    q-block pairs (team B taking the light block and the tail of the heavy
-    one), and the shared K/V stream (256-row blocks, both teams on one staged
-    tile stream, pairs run back to back).  Odd block counts, a kv prefix
-    (pos0 > 0), a single kv head, HG = 3 (rows that fall outside a 126-row
-    block), HG = 7 and HG = 1 (one head per kv group)."""
+    GROUT_FMHA_PREFILL_SHARED / _PAIRED / _WAVE_ROWS: per-team K/V staging
+    with one q block per workgroup (its tiles split over the two 4-wave teams)
+    or complementary q-block pairs (team B taking the light block and the
+    tail of the heavy one), each with 128-row blocks (32 rows per wave) or
+    64-row blocks (16 rows per wave), and the shared K/V stream (256-row
+    blocks, both teams on one staged tile stream, pairs run back to back).
+    Odd block counts, a kv prefix (pos0 > 0), a single kv head, HG = 3 (rows
+    that fall outside a 126- or 63-row block), HG = 7 and HG = 1 (one head
+    per kv group)."""
     monkeypatch.setenv("GROUT_FMHA_PREFILL_SHARED", "1" if mode == "shared" else "0")
-    monkeypatch.setenv("GROUT_FMHA_PREFILL_PAIRED", "1" if mode == "paired" else "0")
+    monkeypatch.setenv("GROUT_FMHA_PREFILL_PAIRED", "1" if mode.startswith("paired") else "0")
+    monkeypatch.setenv("GROUT_FMHA_PREFILL_WAVE_ROWS", "16" if mode.endswith("64") else "32")
     _say("prefill_split", mode, S, Hq, Hkv, pos0)
     max_ctx = pos0 + S + 3
     q = normal(f"wq{S}", (S, Hq, D))
@@ -374,14 +381,16 @@ def test_prefill_work_splits_vs_oracle(gpu, monkeypatch, mode, S, Hq, Hkv, pos0)
     assert_close(got, ref, f"prefill {mode} S={S} Hq={Hq} Hkv={Hkv} pos0={pos0}")
 
 
-@pytest.mark.parametrize("shared", [0, 1])
+@pytest.mark.parametrize("form", ["rows16", "rows32", "shared"])
 @pytest.mark.parametrize("S,pos0", [(77, 0), (130, 61), (1000, 24)])
-def test_prefill_ignores_cache_rows_past_kv_len(gpu, monkeypatch, shared, S, pos0):
+def test_prefill_ignores_cache_rows_past_kv_len(gpu, monkeypatch, form, S, pos0):
     """Cache rows at and past kv_len = pos0 + S hold NaN: the last kv tile
     reads them as zeros (bounded loads) and masks them, so outputs stay equal
-    to the oracle's, which never reads them (per-team and shared staging)."""
-    monkeypatch.setenv("GROUT_FMHA_PREFILL_SHARED", str(shared))
-    _say("prefill_nan_tail", shared, S, pos0)
+    to the oracle's, which never reads them (per-team staging with 64- and
+    128-row blocks, shared staging)."""
+    monkeypatch.setenv("GROUT_FMHA_PREFILL_SHARED", "1" if form == "shared" else "0")
+    monkeypatch.setenv("GROUT_FMHA_PREFILL_WAVE_ROWS", "32" if form == "rows32" else "16")
+    _say("prefill_nan_tail", form, S, pos0)
     Hq, Hkv, max_ctx = 32, 8, pos0 + S + 70
     q = normal(f"nt{S}", (S, Hq, D))
     kc, vc = normal(f"ntk{S}", (Hkv, max_ctx, D)), normal(f"ntv{S}", (Hkv, max_ctx, D))
@@ -391,7 +400,7 @@ def test_prefill_ignores_cache_rows_past_kv_len(gpu, monkeypatch, shared, S, pos
     ref = O.attention_prefill_rows(q, kc, vc, pos0, nthreads=16)
     out = gpu.ops.fmha_prefill(dev(q), dev(kc), dev(vc), pos0)
     torch.cuda.synchronize()
-    assert_close(host_f32(out), ref, f"prefill nan tail shared={shared} S={S} pos0={pos0}")
+    assert_close(host_f32(out), ref, f"prefill nan tail {form} S={S} pos0={pos0}")
 
 
 # ------------------------------------------------------- configs end to end
