@@ -959,10 +959,8 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_shared_kernel(
 // GROUT_FMHA_PREFILL_PAIRED=0/1 forces the single-block / paired work split
 // of the per-team kernel, GROUT_FMHA_PREFILL_WAVE_ROWS=16/32 its 64-row /
 // 128-row blocks, GROUT_FMHA_PREFILL_SHARED=0/1 the per-team / shared-stream
-// kernel (tests exercise every form).  By default the shared stream is used
-// when its block pairs fill the GPU (one workgroup per CU, 256 CUs), else the
-// per-team kernel with 128-row blocks when their pairs fill it, else with
-// 64-row blocks, paired when those pairs fill it, else single blocks.
+// kernel (tests exercise every form); launch_fmha_prefill picks one by
+// default.
 static int env_override(const char* name) {
   const char* e = std::getenv(name);
   return e ? std::atoi(e) : -1;
@@ -976,24 +974,42 @@ hipError_t launch_fmha_prefill(const void* q, const void* k_cache, const void* v
   int HG = 8;
   while (G % HG != 0) --HG;
   const int BQ = kRowsPerTeam / HG;
-  const int nqb = (seq_len + BQ - 1) / BQ;
   const int per_block = Hkv * (G / HG);
-  // Complementary pairs give every workgroup the same work; they are used
-  // when there are enough of them for one workgroup per CU (256 CUs).
-  const long pair_blocks = (long)((nqb + 1) / 2) * per_block;
-  // shared stream: 256-row blocks of 2*BQ positions, complementary pairs
+  // Work splits (one 512-thread workgroup per CU at a time, 256 CUs).  Pairs
+  // of complementary blocks give every workgroup the same work, so a pair
+  // form is taken when its workgroups fill the CUs: 192-256 of them (one
+  // round), or at least 90% of the CU rounds they take (a second round that is
+  // only partly full costs a whole pair's time).  Large blocks first (less
+  // staging per FLOP): the shared stream (256-row blocks), per-team 128-row
+  // pairs, per-team 64-row pairs (one round only: their half-size MFMA work
+  // per tile loses to 128-row blocks once the GPU is full).  Otherwise single
+  // blocks, heaviest first, which the dispatcher balances like a longest-first
+  // list schedule: 128-row blocks when there are at least 192 of them, else
+  // 64-row blocks.  Measured over S = 256-8192 at G = 4 and 8 (Qwen3-4B and
+  // -32B heads): the pick is the fastest form or within 2% of it at every
+  // length.
+  constexpr long kCUs = 256;
+  auto fills = [&](long wgs) {
+    if (wgs <= kCUs) return 4 * wgs >= 3 * kCUs;
+    const long rounds = (wgs + kCUs - 1) / kCUs;
+    return 10 * wgs >= 9 * kCUs * rounds;
+  };
+  auto blocks_of = [&](int bq) { return (long)((seq_len + bq - 1) / bq) * per_block; };
+  auto pairs_of = [&](int bq) { return (long)(((seq_len + bq - 1) / bq + 1) / 2) * per_block; };
+  const int BQ64 = (kRowsPerTeam / 2) / HG;  // positions per 64-row block
   const int nqb2 = (seq_len + 2 * BQ - 1) / (2 * BQ);
-  const long shared_blocks = (long)((nqb2 + 1) / 2) * per_block;
-  int shared = shared_blocks >= 256 ? 1 : 0;
+  const long shared_blocks = pairs_of(2 * BQ);
+  int shared = fills(shared_blocks) ? 1 : 0;
   if (const int o = env_override("GROUT_FMHA_PREFILL_SHARED"); o == 0 || o == 1) shared = o;
-  // 64-row blocks (16 rows per wave) when 128-row pairs would leave CUs idle
-  int wave_rows = pair_blocks >= 256 ? 32 : 16;
+  auto pairs_fill = [&](int rows) {
+    return rows == 32 ? fills(pairs_of(BQ)) : pairs_of(BQ64) <= kCUs && fills(pairs_of(BQ64));
+  };
+  int wave_rows = pairs_fill(32) ? 32 : pairs_fill(16) ? 16 : blocks_of(BQ) >= 3 * kCUs / 4 ? 32 : 16;
   if (const int o = env_override("GROUT_FMHA_PREFILL_WAVE_ROWS"); o == 16 || o == 32)
     wave_rows = o;
-  const int BQr = wave_rows == 32 ? BQ : (kRowsPerTeam / 2) / HG;
+  const int BQr = wave_rows == 32 ? BQ : BQ64;
   const int nqbr = (seq_len + BQr - 1) / BQr;
-  const long pair_blocks_r = (long)((nqbr + 1) / 2) * per_block;
-  int paired = pair_blocks_r >= 256 ? 1 : 0;
+  int paired = pairs_fill(wave_rows) ? 1 : 0;
   if (const int o = env_override("GROUT_FMHA_PREFILL_PAIRED"); o == 0 || o == 1) paired = o;
   const long blocks =
       shared ? shared_blocks : (paired ? (nqbr + 1) / 2 : nqbr) * (long)per_block;
