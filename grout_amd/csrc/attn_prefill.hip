@@ -26,9 +26,9 @@
 //    and l = r (their tile counts add up to a constant).  Team A takes tiles
 //    [0, a) of h, team B all tiles of l and then tiles [a, T_h) of h, with
 //    a = ceil((T_h + T_l) / 2); the two partials (m, l, acc) of h meet in
-//    LDS at the end and each team finishes half of h's d range.  With too
-//    few pairs to fill the GPU each
-//    workgroup takes a single q block (T_l = 0), heaviest first;
+//    LDS at the end and each team finishes half of h's d range.  Or each
+//    workgroup takes a single q block (T_l = 0), heaviest first (the work
+//    split is chosen per launch, see launch_fmha_prefill);
 //  * K and V tiles (64 positions, 16 KiB each) go straight from the cache into
 //    double-buffered, XOR-swizzled LDS slots with buffer_load ... lds.  A
 //    per-tile buffer resource bounds the read at kv_len, so rows past the end
