@@ -314,6 +314,7 @@ def bench_prefill(ops, S, Hq, Hkv, steps, warmup):
     ms = time_launches(call, steps, warmup, torch.cuda.current_stream(dev))
     flop = 4.0 * Hq * D * S * (S + 1) / 2
     return dict(ms=ms, flop=flop, dist=time_distribution(call, calls=100),
+                plan=ops.prefill_plan(S, Hq, Hkv),
                 library=bench_prefill_library(q, kc, vc, out, steps, warmup))
 
 
@@ -883,13 +884,14 @@ def main():
         line["prefill"] = {"workload": "qwen3-4b causal prefill FMHA S=2048 Hq=32 Hkv=8 D=128",
                            "us": round(r["ms"] * 1e3, 2), "tflops": round(tf, 1),
                            "mfma_frac": round(tf / F16_MFMA_PEAK_TFLOPS, 4),
-                           "flop": r["flop"], "us_source": PREFILL_US_SOURCE, "us_dist": r["dist"]}
+                           "flop": r["flop"], "us_source": PREFILL_US_SOURCE, "us_dist": r["dist"],
+                           "work_split": r["plan"]}
         sweep = {}
         for S, rr in res["prefill_sweep"].items():
             t = rr["flop"] / (rr["ms"] * 1e-3) / 1e12
             sweep[str(S)] = {"us": round(rr["ms"] * 1e3, 2), "tflops": round(t, 1),
                              "mfma_frac": round(t / F16_MFMA_PEAK_TFLOPS, 4), "flop": rr["flop"],
-                             "us_dist": rr["dist"]}
+                             "us_dist": rr["dist"], "work_split": rr["plan"]}
             lib = rr.get("library") or {}
             if "ms" in lib:
                 lt = rr["flop"] / (lib["ms"] * 1e-3) / 1e12

@@ -81,6 +81,7 @@ SIGNATURES = {
                                           _f, _p]),
     "grout_fmha_prefill": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i, _l, _f, _p]),
     "grout_attn_decode_default_splits": (_i, [_i, _i, _i]),
+    "grout_fmha_prefill_plan": (_i, [_i, _i, _i, _p, _p, _p]),
     "grout_attn_decode_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "grout_attn_decode": (_i, [_p, _p, _p, _p, _p, _sz, _p, _i, _i, _i, _i, _l, _i, _f, _p]),
     "grout_attn_decode_noalloc": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _i, _l, _i, _f, _p]),

@@ -959,17 +959,13 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_shared_kernel(
 // GROUT_FMHA_PREFILL_PAIRED=0/1 forces the single-block / paired work split
 // of the per-team kernel, GROUT_FMHA_PREFILL_WAVE_ROWS=16/32 its 64-row /
 // 128-row blocks, GROUT_FMHA_PREFILL_SHARED=0/1 the per-team / shared-stream
-// kernel (tests exercise every form); launch_fmha_prefill picks one by
-// default.
+// kernel (tests exercise every form); plan_fmha_prefill picks one by default.
 static int env_override(const char* name) {
   const char* e = std::getenv(name);
   return e ? std::atoi(e) : -1;
 }
 
-hipError_t launch_fmha_prefill(const void* q, const void* k_cache, const void* v_cache,
-                               void* out, int seq_len, int pos0, int Hq, int Hkv,
-                               long head_stride, float qk_scale, hipStream_t stream) {
-  const float scale_log2 = qk_scale * 1.4426950408889634f;
+PrefillPlan plan_fmha_prefill(int seq_len, int Hq, int Hkv) {
   const int G = Hq / Hkv;
   int HG = 8;
   while (G % HG != 0) --HG;
@@ -997,22 +993,34 @@ hipError_t launch_fmha_prefill(const void* q, const void* k_cache, const void* v
   auto blocks_of = [&](int bq) { return (long)((seq_len + bq - 1) / bq) * per_block; };
   auto pairs_of = [&](int bq) { return (long)(((seq_len + bq - 1) / bq + 1) / 2) * per_block; };
   const int BQ64 = (kRowsPerTeam / 2) / HG;  // positions per 64-row block
-  const int nqb2 = (seq_len + 2 * BQ - 1) / (2 * BQ);
-  const long shared_blocks = pairs_of(2 * BQ);
-  int shared = fills(shared_blocks) ? 1 : 0;
-  if (const int o = env_override("GROUT_FMHA_PREFILL_SHARED"); o == 0 || o == 1) shared = o;
+  PrefillPlan p;
+  p.HG = HG;
+  p.nqb2 = (seq_len + 2 * BQ - 1) / (2 * BQ);
+  p.shared = fills(pairs_of(2 * BQ));
+  if (const int o = env_override("GROUT_FMHA_PREFILL_SHARED"); o == 0 || o == 1) p.shared = o;
   auto pairs_fill = [&](int rows) {
     return rows == 32 ? fills(pairs_of(BQ)) : pairs_of(BQ64) <= kCUs && fills(pairs_of(BQ64));
   };
-  int wave_rows = pairs_fill(32) ? 32 : pairs_fill(16) ? 16 : blocks_of(BQ) >= 3 * kCUs / 4 ? 32 : 16;
+  p.wave_rows =
+      pairs_fill(32) ? 32 : pairs_fill(16) ? 16 : blocks_of(BQ) >= 3 * kCUs / 4 ? 32 : 16;
   if (const int o = env_override("GROUT_FMHA_PREFILL_WAVE_ROWS"); o == 16 || o == 32)
-    wave_rows = o;
-  const int BQr = wave_rows == 32 ? BQ : BQ64;
-  const int nqbr = (seq_len + BQr - 1) / BQr;
-  int paired = pairs_fill(wave_rows) ? 1 : 0;
-  if (const int o = env_override("GROUT_FMHA_PREFILL_PAIRED"); o == 0 || o == 1) paired = o;
-  const long blocks =
-      shared ? shared_blocks : (paired ? (nqbr + 1) / 2 : nqbr) * (long)per_block;
+    p.wave_rows = o;
+  const int BQr = p.wave_rows == 32 ? BQ : BQ64;
+  p.nqb = (seq_len + BQr - 1) / BQr;
+  p.paired = pairs_fill(p.wave_rows);
+  if (const int o = env_override("GROUT_FMHA_PREFILL_PAIRED"); o == 0 || o == 1) p.paired = o;
+  p.workgroups = p.shared ? pairs_of(2 * BQ) : (p.paired ? (p.nqb + 1) / 2 : p.nqb) * (long)per_block;
+  return p;
+}
+
+hipError_t launch_fmha_prefill(const void* q, const void* k_cache, const void* v_cache,
+                               void* out, int seq_len, int pos0, int Hq, int Hkv,
+                               long head_stride, float qk_scale, hipStream_t stream) {
+  const float scale_log2 = qk_scale * 1.4426950408889634f;
+  const PrefillPlan p = plan_fmha_prefill(seq_len, Hq, Hkv);
+  const long blocks = p.workgroups;
+  const int shared = p.shared, wave_rows = p.wave_rows, paired = p.paired, nqbr = p.nqb,
+            nqb2 = p.nqb2;
   if (blocks <= 0 || blocks > 0x7fffffffL) return hipErrorInvalidValue;
 #define GROUT_PREFILL_CASE(hg)                                                             \
   case hg:                                                                                 \
@@ -1029,7 +1037,7 @@ hipError_t launch_fmha_prefill(const void* q, const void* k_cache, const void* v
           (const half_t*)q, (const half_t*)k_cache, (const half_t*)v_cache, (half_t*)out,  \
           seq_len, pos0, Hq, Hkv, head_stride, scale_log2, nqbr, paired);                  \
     break;
-  switch (HG) {
+  switch (p.HG) {
     GROUT_PREFILL_CASE(1)
     GROUT_PREFILL_CASE(2)
     GROUT_PREFILL_CASE(3)

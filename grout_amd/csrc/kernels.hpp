@@ -46,6 +46,16 @@ hipError_t launch_attn_decode_merge(const float* part_acc, const float* part_ml,
                                     int Hq, int Hkv, int nsplit, hipStream_t stream,
                                     uint32_t* advance_pos = nullptr);
 
+// Work split of the causal prefill FMHA for one launch (host side, no GPU):
+// shared K/V stream (256-row q blocks, pairs) or the per-team kernel with
+// wave_rows = 32 (128-row blocks) or 16 (64-row blocks), single blocks or
+// complementary pairs; HG heads per q block, nqb (nqb2) blocks per kv head
+// group of the per-team (shared) form, workgroups = grid size.
+struct PrefillPlan {
+  int HG = 1, shared = 0, wave_rows = 32, paired = 0, nqb = 0, nqb2 = 0;
+  long workgroups = 0;
+};
+PrefillPlan plan_fmha_prefill(int seq_len, int Hq, int Hkv);
 hipError_t launch_fmha_prefill(const void* q, const void* k_cache, const void* v_cache,
                                void* out, int seq_len, int pos0, int Hq, int Hkv,
                                long head_stride, float qk_scale, hipStream_t stream);

@@ -109,6 +109,21 @@ def fmha_prefill(q, k_cache, v_cache, position_start: int, out=None,
     return out
 
 
+PREFILL_FORMS = {0: "shared K/V stream, 256-row q blocks", 1: "per-team, 128-row q blocks",
+                 2: "per-team, 64-row q blocks"}
+
+
+def prefill_plan(seq_len: int, num_q_heads: int, num_kv_heads: int) -> dict:
+    """The work split grout_fmha_prefill launches for these shapes (host only)."""
+    import ctypes as C
+
+    form, paired, wgs = C.c_int(), C.c_int(), C.c_long()
+    call("grout_fmha_prefill_plan", seq_len, num_q_heads, num_kv_heads, C.byref(form),
+         C.byref(paired), C.byref(wgs))
+    return dict(form=form.value, name=PREFILL_FORMS[form.value], paired=bool(paired.value),
+                workgroups=int(wgs.value))
+
+
 def default_splits(ctx_len: int, num_q_heads: int, num_kv_heads: int) -> int:
     return int(lib().grout_attn_decode_default_splits(ctx_len, num_q_heads, num_kv_heads))
 

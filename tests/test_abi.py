@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import grout_amd
-from grout_amd import _lib
+from grout_amd import _lib, ops
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "*.h")))
@@ -149,6 +149,46 @@ def test_argument_validation_without_gpu():
     # NULL position pointer
     rc = L.grout_fmha_decode_gqa_split(p, p, p, p, p, None, 8, 2, 128, 64, 64 * 128, 2, 0.088, None)
     assert rc == -1 and "d_pos" in _lib.last_error()
+
+
+# Qwen3-4B (32 / 8 heads) and Qwen3-32B (64 / 8): the pick at each length, the
+# fastest of the five forms in a sweep on MI355X (form 0 shared stream, 1 per-team
+# 128-row blocks, 2 per-team 64-row blocks; paired; workgroups).
+PREFILL_PLANS = {
+    (256, 32): (2, 0, 128), (512, 32): (2, 0, 256), (768, 32): (2, 1, 192),
+    (1024, 32): (2, 1, 256), (1280, 32): (1, 0, 320), (1536, 32): (1, 1, 192),
+    (2048, 32): (1, 1, 256), (2560, 32): (1, 0, 640), (3072, 32): (0, 1, 192),
+    (4096, 32): (0, 1, 256), (5120, 32): (1, 0, 1280), (6144, 32): (1, 1, 768),
+    (8192, 32): (0, 1, 512),
+    (256, 64): (2, 0, 256), (512, 64): (2, 1, 256), (768, 64): (1, 1, 192),
+    (1024, 64): (1, 1, 256), (1536, 64): (0, 1, 192), (2048, 64): (0, 1, 256),
+    (3072, 64): (1, 1, 768), (4096, 64): (0, 1, 512),
+}
+
+
+@pytest.mark.parametrize("S,Hq", sorted(PREFILL_PLANS))
+def test_prefill_work_split_plan(monkeypatch, S, Hq):
+    for k in ("SHARED", "PAIRED", "WAVE_ROWS"):
+        monkeypatch.delenv("GROUT_FMHA_PREFILL_" + k, raising=False)
+    p = ops.prefill_plan(S, Hq, 8)
+    assert (p["form"], int(p["paired"]), p["workgroups"]) == PREFILL_PLANS[(S, Hq)]
+
+
+def test_prefill_plan_overrides_and_errors(monkeypatch):
+    monkeypatch.setenv("GROUT_FMHA_PREFILL_SHARED", "1")
+    assert ops.prefill_plan(512, 32, 8)["form"] == 0
+    monkeypatch.setenv("GROUT_FMHA_PREFILL_SHARED", "0")
+    monkeypatch.setenv("GROUT_FMHA_PREFILL_WAVE_ROWS", "32")
+    monkeypatch.setenv("GROUT_FMHA_PREFILL_PAIRED", "0")
+    p = ops.prefill_plan(2048, 32, 8)
+    assert (p["form"], p["paired"], p["workgroups"]) == (1, False, 512)
+    monkeypatch.setenv("GROUT_FMHA_PREFILL_WAVE_ROWS", "16")
+    monkeypatch.setenv("GROUT_FMHA_PREFILL_PAIRED", "1")
+    p = ops.prefill_plan(2048, 32, 8)
+    assert (p["form"], p["paired"], p["workgroups"]) == (2, True, 512)
+    L = grout_amd.lib()
+    assert L.grout_fmha_prefill_plan(0, 32, 8, None, None, None) == -1
+    assert L.grout_fmha_prefill_plan(16, 30, 8, None, None, None) == -1
 
 
 def test_decode_split_defaults_and_workspace():
