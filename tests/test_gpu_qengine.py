@@ -113,6 +113,33 @@ def test_qengine_extend_and_greedy_vs_oracle(gpu):
         eng.close()
 
 
+def test_qengine_warmup_leaves_a_fresh_session(gpu):
+    """grout_engine_warmup on a mixed-format engine: after a session, the
+    warmup's one-token prefill (dequant + GEMM path) and decode-graph replay,
+    then the reset, leave position 0, and the next prefill and greedy steps
+    equal a fresh engine's bit for bit."""
+    cfg, eng, _ = build("k1024", "q4km-tied", 21, 256)
+    _, fresh, _ = build("k1024", "q4km-tied", 21, 256)
+    rng = np.random.default_rng(8)
+    try:
+        eng.prefill(rng.integers(0, cfg.vocab_size, 9))
+        eng.decode_greedy(5)
+        eng.warmup()
+        assert eng.position == 0
+        prompt = rng.integers(0, cfg.vocab_size, 30)
+        a, b = eng.prefill(prompt).values, fresh.prefill(prompt).values
+        assert np.array_equal(a, b)
+        tok = int(np.argmax(a))
+        for i in range(3):
+            ta, tb = eng.decode_greedy(tok), fresh.decode_greedy(tok)
+            assert ta == tb, f"step {i}"
+            tok = ta
+        assert eng.position == fresh.position == 33
+    finally:
+        eng.close()
+        fresh.close()
+
+
 def test_qengine_argument_errors(gpu):
     """Shape, format and part-layout errors are reported by name."""
     import ctypes as C
