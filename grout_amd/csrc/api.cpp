@@ -117,7 +117,8 @@ int grout_fmha_prefill(const void* q, const void* k_cache, const void* v_cache, 
 int grout_fmha_prefill_plan(int seq_len, int num_q_heads, int num_kv_heads, int* form,
                             int* paired, long* workgroups) {
   GROUT_CHECK(check_heads(num_q_heads, num_kv_heads, 128, 1 << 20));
-  GROUT_NEED(seq_len >= 1, GROUT_EINVAL, "attention requires q_len >= 1");
+  GROUT_NEED(seq_len >= 1 && seq_len <= GROUT_MAX_CTX, GROUT_EINVAL,
+             "seq_len=%d outside [1, GROUT_MAX_CTX=%d]", seq_len, GROUT_MAX_CTX);
   const grout::PrefillPlan p = grout::plan_fmha_prefill(seq_len, num_q_heads, num_kv_heads);
   if (form) *form = p.shared ? 0 : p.wave_rows == 32 ? 1 : 2;
   if (paired) *paired = p.shared ? 1 : p.paired;

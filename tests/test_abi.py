@@ -188,6 +188,7 @@ def test_prefill_plan_overrides_and_errors(monkeypatch):
     assert (p["form"], p["paired"], p["workgroups"]) == (2, True, 512)
     L = grout_amd.lib()
     assert L.grout_fmha_prefill_plan(0, 32, 8, None, None, None) == -1
+    assert L.grout_fmha_prefill_plan((1 << 22) + 1, 32, 8, None, None, None) == -1
     assert L.grout_fmha_prefill_plan(16, 30, 8, None, None, None) == -1
 
 
