@@ -76,7 +76,31 @@ def build(verbose: bool = False, resource_usage: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}{r.stderr}")
     os.replace(tmp, LIB)
+    _build_examples(verbose)
     return LIB
+
+
+EXAMPLES = os.path.join(HERE, "examples")
+INCLUDE = os.path.join(os.path.dirname(HERE), "include")
+
+
+def _build_examples(verbose: bool) -> None:
+    """Host programs over the C++ API (include/grout.hpp), linked against the
+    library just built; they find it next to them at run time."""
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if cxx is None:
+        raise RuntimeError("g++ not found: the C++ examples cannot be built")
+    src = os.path.join(EXAMPLES, "generate.cpp")
+    out = os.path.join(EXAMPLES, "grout_generate")
+    cmd = [cxx, "-std=c++17", "-O2", "-Wall", "-Wextra", "-Werror", "-pedantic", f"-I{INCLUDE}",
+           src, f"-L{HERE}", "-lgrout_attn", "-Wl,-rpath,$ORIGIN/..",
+           "-Wl,-rpath-link,/opt/rocm/lib", "-o", out + ".tmp"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"example build failed:\n{r.stdout}{r.stderr}")
+    os.replace(out + ".tmp", out)
 
 
 def main(argv=None) -> int:

@@ -22,6 +22,47 @@ def header_functions():
     return sorted(set(names))
 
 
+EXAMPLE = os.path.join(ROOT, "grout_amd", "examples", "grout_generate")
+
+
+def test_cpp_api_header_compiles_strictly(tmp_path):
+    """include/grout.hpp (the C++ mirror of the reference's Engine API) as a
+    C++17 caller sees it: -Wall -Wextra -Werror -pedantic."""
+    import shutil
+    import subprocess
+
+    cxx = shutil.which("g++")
+    if cxx is None:
+        pytest.skip("g++ not found")
+    src = tmp_path / "use.cpp"
+    src.write_text('#include "grout.hpp"\n'
+                   "int main() {\n"
+                   "  grout::LoadOpts o; grout::Logits l; grout::ModelMeta m;\n"
+                   "  (void)o; (void)l.as_slice(); (void)m;\n"
+                   "  return std::is_nothrow_move_constructible<grout::Engine>::value ? 0 : 1;\n"
+                   "}\n")
+    r = subprocess.run([cxx, "-std=c++17", "-Wall", "-Wextra", "-Werror", "-pedantic",
+                        "-include", "type_traits", f"-I{os.path.join(ROOT, 'include')}",
+                        "-fsyntax-only", str(src)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
+def test_cpp_example_reports_errors_before_any_gpu_call():
+    """grout_amd/examples/grout_generate (built with the library) reports a
+    missing model directory, bad arguments and usage without touching a GPU."""
+    import subprocess
+
+    assert os.path.exists(EXAMPLE), "run `python -m grout_amd.build` first"
+    r = subprocess.run([EXAMPLE, "/nonexistent-model-dir", "16", "1", "3"], capture_output=True,
+                       text=True, timeout=60)
+    assert r.returncode == 1 and "grout error -1" in r.stderr and "config.json" in r.stderr
+    r = subprocess.run([EXAMPLE, "/nonexistent-model-dir", "16", "x", "3"], capture_output=True,
+                       text=True, timeout=60)
+    assert r.returncode == 1 and "bad n_decode" in r.stderr
+    r = subprocess.run([EXAMPLE], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 2 and "usage" in r.stderr
+
+
 def test_library_is_built_and_loads():
     assert os.path.exists(grout_amd.LIB_PATH), "run `python -m grout_amd.build` first"
     L = grout_amd.lib()

@@ -14,6 +14,7 @@ Tolerances:
     max-abs tolerance.
 """
 import ctypes as C
+import os
 
 import numpy as np
 import pytest
@@ -720,3 +721,46 @@ def test_engine_load_matches_oracle(gpu, tmp_path):
         assert np.array_equal(eng.prefill(prompt).values, first)
     finally:
         eng.close()
+
+
+def test_cpp_engine_api_generates_against_the_oracle(gpu, tmp_path):
+    """The C++ host API (include/grout.hpp) in its own process: the example
+    program grout_generate loads a checkpoint directory, warms up, prefills
+    and decodes greedily.  Its meta is the checkpoint's, its prefill logits
+    are within the engine tolerance of the oracle, and every greedy token is
+    the oracle's argmax on the tokens so far (teacher-forced).  (A process
+    that imported torch first binds the library to torch's bundled HIP
+    runtime and rocBLAS, which share the sonames of /opt/rocm's, so the
+    prefill GEMMs of this program and of the Python mirror may round apart;
+    both are held to the oracle.)"""
+    import subprocess
+
+    from ckpt_util import write_checkpoint
+    from grout_amd.model import Qwen3Config
+
+    exe = os.path.join(os.path.dirname(gpu.LIB_PATH), "examples", "grout_generate")
+    assert os.path.exists(exe), "run `python -m grout_amd.build` first"
+    cfg = Qwen3Config(num_layers=2, hidden_size=512, intermediate_size=1024,
+                      num_attention_heads=8, num_key_value_heads=2, vocab_size=1000)
+    host_w = write_checkpoint(tmp_path, cfg, seed=19, dtypes=("BF16",), shards=1, max_pos=256,
+                              generation_eos=[5])
+    prompt = [int(t) for t in np.random.default_rng(11).integers(0, 1000, 33)]
+    n_decode = 6
+    print("cpp generate: child process", flush=True)
+    r = subprocess.run([exe, str(tmp_path), "128", str(n_decode), *map(str, prompt)],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    lines = dict(l.split(" ", 1) for l in r.stdout.strip().splitlines())
+    assert lines["meta"] == "vocab=1000 max_ctx=128 arch=qwen3 eos=5"
+    cpp_logits = np.array([float.fromhex(x) for x in lines["prefill_logits"].split()],
+                          dtype=np.float32)
+    cpp_tokens = [int(t) for t in lines["tokens"].split()]
+    assert len(cpp_tokens) == n_decode + 1
+    assert int(lines["position"]) == len(prompt) + n_decode
+    orc = Q.Qwen3Oracle(cfg, host_w, 128)
+    ref, _ = orc.prefill(prompt, nthreads=8)
+    tol = check_logits(cpp_logits, ref, "C++ prefill")
+    check_token(cpp_tokens[0], ref, tol, "C++ prefill token")
+    for i, (tok, nxt) in enumerate(zip(cpp_tokens[:-1], cpp_tokens[1:])):
+        ref, _ = orc.decode(tok, nthreads=8)
+        check_token(nxt, ref, tol, f"C++ greedy step {i}")
