@@ -478,6 +478,42 @@ def test_prefill_row_equals_decode_at_same_position(gpu):
 # ------------------------------------------------------------- decode graph
 
 
+def test_ops_run_on_the_callers_stream(gpu):
+    """Every call works on the stream it is given: the fused prefill write,
+    the prefill FMHA, split-K decode and the fused decode layer issued on a
+    side stream (default priority), each behind a host-visible dependency on
+    that stream only, equal the same calls on the default stream bit for
+    bit."""
+    Hq, Hkv, S, max_ctx = 32, 8, 300, 1024
+    _say("side stream")
+    q, k, v = normal("ssq", (S, Hq, D)), normal("ssk", (S, Hkv, D)), normal("ssv", (S, Hkv, D))
+    gq, gk = dev(gamma("ssgq")), dev(gamma("ssgk"))
+    qkv = dev(normal("ssqkv", ((Hq + 2 * Hkv) * D,)))
+    rope = gpu.ops.rope_tables(max_ctx)
+    qd, kd, vd = dev(q), dev(k), dev(v)
+
+    def run():
+        kc = torch.zeros((Hkv, max_ctx, D), dtype=torch.float16, device="cuda")
+        vc = torch.zeros_like(kc)
+        qr = gpu.ops.qk_norm_rope_kv_prefill(qd, kd, vd, gq, gk, rope, kc, vc, 0)
+        pre = gpu.ops.fmha_prefill(qr, kc, vc, 0)
+        p = torch.tensor([S], dtype=torch.int32, device="cuda")
+        fused = gpu.ops.attn_decode_fused(qkv, gq, gk, rope, kc, vc, p, Hq)
+        dec = gpu.ops.attn_decode(pre[-1], kc, vc, p, num_splits=7)
+        return [pre, fused, dec, kc, vc]
+
+    ref = run()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        torch.cuda._sleep(1 << 20)  # the side stream is busy first: a call on the
+        got = run()                 # default stream instead would read unfinished inputs
+    side.synchronize()
+    for i, (a, b) in enumerate(zip(ref, got)):
+        assert torch.equal(a, b), f"output {i} differs on the side stream"
+
+
 def test_decode_graph_replays_match_eager_ops(gpu):
     from grout_amd.engine import AttentionConfig, AttentionEngine
 
