@@ -431,6 +431,53 @@ def test_engine_sequential_decode_fallback_matches_graph(gpu, monkeypatch):
         seq.close()
 
 
+def test_two_engines_in_two_threads_match_sequential_runs(gpu):
+    """Engines are independent (own stream, caches, workspace and graph): two
+    of them driven from two threads at once, each through prefill and greedy
+    decode several times, give exactly the sequential runs' tokens and
+    logits (the calls release the GIL, so the work overlaps)."""
+    import threading
+
+    cfg = tiny_configs()["g8"]
+    ws = [Q.random_host_weights(cfg, seed=s, std=0.05) for s in (31, 32)]
+    prompts = [[3, 9, 27, 81, 243, 5, 6], [11, 12, 13, 400, 7]]
+
+    def session(eng, prompt):
+        out = []
+        for _ in range(3):
+            lg = eng.prefill(prompt).values
+            toks = [int(np.argmax(lg))]
+            for _ in range(6):
+                toks.append(eng.decode_greedy(toks[-1]))
+            out.append((lg, toks))
+        return out
+
+    engines = [make_engine(cfg, w, 64) for w in ws]
+    try:
+        seq = [session(e, p) for e, p in zip(engines, prompts)]
+        got = [None, None]
+        errors = []
+
+        def worker(i):
+            try:
+                got[i] = session(engines[i], prompts[i])
+            except Exception as ex:  # noqa: BLE001 - reported below
+                errors.append(ex)
+
+        threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join(timeout=120)
+        assert not errors, errors
+        for i in range(2):
+            for (la, ta), (lb, tb) in zip(seq[i], got[i]):
+                assert np.array_equal(la, lb) and ta == tb, f"engine {i}"
+    finally:
+        for e in engines:
+            e.close()
+
+
 def test_engine_warmup_leaves_a_fresh_session(gpu):
     """grout_engine_warmup (src/api.rs:153-162): one-token steps at positions 0
     and 1, then the in-place reset: position 0, no session, and the next
