@@ -514,6 +514,58 @@ def test_ops_run_on_the_callers_stream(gpu):
         assert torch.equal(a, b), f"output {i} differs on the side stream"
 
 
+def test_ops_captured_by_the_caller_replay_like_eager_calls(gpu):
+    """The calls are capture-safe: the fused decode layer, split-K decode and
+    the prefill FMHA captured into a caller's HIP graph (torch), replayed
+    several times with the program's own eager work (new inputs, a new
+    position) and host synchronizations between the replays, match eager
+    calls on the same inputs bit for bit at every replay."""
+    Hq, Hkv, S, max_ctx = 32, 8, 200, 1024
+    _say("caller graph")
+    gq, gk = dev(gamma("cggq")), dev(gamma("cggk"))
+    rope = gpu.ops.rope_tables(max_ctx)
+    kc = dev(normal("cgk", (Hkv, max_ctx, D)))
+    vc = dev(normal("cgv", (Hkv, max_ctx, D)))
+    qkv = torch.empty(((Hq + 2 * Hkv) * D,), dtype=torch.float16, device="cuda")
+    qp = torch.empty((S, Hq, D), dtype=torch.float16, device="cuda")
+    pos = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ws = gpu.ops.decode_workspace(Hq, Hkv, 16, "cuda")
+    ws2 = gpu.ops.decode_workspace(Hq, Hkv, 5, "cuda")
+    outs = [torch.empty((Hq, D), dtype=torch.float16, device="cuda") for _ in range(2)]
+    pre = torch.empty_like(qp)
+
+    def body(kc_, vc_, o0, o1, pr):
+        gpu.ops.attn_decode_fused(qkv, gq, gk, rope, kc_, vc_, pos, Hq, num_splits=16, out=o0,
+                                  workspace=ws)
+        gpu.ops.attn_decode(qkv[:Hq * D].view(Hq, D), kc_, vc_, pos, num_splits=5, out=o1,
+                            workspace=ws2)
+        gpu.ops.fmha_prefill(qp, kc_, vc_, 0, out=pr)
+
+    qkv.copy_(dev(normal("cgqkv0", ((Hq + 2 * Hkv) * D,))))
+    qp.copy_(dev(normal("cgq0", (S, Hq, D))))
+    body(kc.clone(), vc.clone(), *[torch.empty_like(o) for o in outs], torch.empty_like(pre))
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    kg, vg = kc.clone(), vc.clone()
+    with torch.cuda.graph(g):
+        body(kg, vg, outs[0], outs[1], pre)
+    for rep, p in enumerate([300, 301, 57, 900]):
+        qkv.copy_(dev(normal(f"cgqkv{rep}", ((Hq + 2 * Hkv) * D,))))
+        qp.copy_(dev(normal(f"cgq{rep}", (S, Hq, D))))
+        pos.fill_(p)
+        ke, ve = kg.clone(), vg.clone()  # eager reference from the same cache state
+        torch.cuda.synchronize()
+        g.replay()
+        eo = [torch.empty_like(o) for o in outs]
+        ep = torch.empty_like(pre)
+        body(ke, ve, eo[0], eo[1], ep)
+        torch.cuda.synchronize()
+        assert torch.equal(kg, ke) and torch.equal(vg, ve), f"replay {rep}: caches"
+        assert torch.equal(outs[0], eo[0]) and torch.equal(outs[1], eo[1]), f"replay {rep}: decode"
+        assert torch.equal(pre, ep), f"replay {rep}: prefill"
+    del g
+
+
 def test_decode_graph_replays_match_eager_ops(gpu):
     from grout_amd.engine import AttentionConfig, AttentionEngine
 
