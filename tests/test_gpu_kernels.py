@@ -354,7 +354,7 @@ def test_prefill_random_shapes_vs_oracle(gpu, monkeypatch, form, S, Hq, Hkv, pos
 @pytest.mark.parametrize("S,Hq,Hkv,pos0", [
     (1, 32, 8, 0), (17, 32, 8, 0), (130, 64, 8, 0), (200, 32, 8, 77), (77, 40, 8, 9),
     (33, 16, 1, 0), (700, 32, 8, 100), (1000, 16, 4, 0), (2048, 24, 8, 0), (600, 56, 8, 7),
-    (3000, 32, 8, 0), (523, 8, 8, 300), (300, 48, 8, 20), (400, 16, 8, 0)])
+    (3000, 32, 8, 0), (523, 8, 8, 300), (300, 48, 8, 20), (400, 16, 8, 0), (260, 64, 2, 31)])
 def test_prefill_work_splits_vs_oracle(gpu, monkeypatch, mode, S, Hq, Hkv, pos0):
     """Every work split of the prefill FMHA, forced through
     GROUT_FMHA_PREFILL_SHARED / _PAIRED / _WAVE_ROWS: per-team K/V staging
@@ -365,7 +365,8 @@ def test_prefill_work_splits_vs_oracle(gpu, monkeypatch, mode, S, Hq, Hkv, pos0)
     blocks, both teams on one staged tile stream, pairs run back to back).
     Odd block counts, a kv prefix (pos0 > 0), a single kv head, HG = 3 (rows
     that fall outside a 126- or 63-row block), HG = 5, 6 and 7 (60-63 of 64
-    rows used), HG = 2 and HG = 1 (one head per kv group)."""
+    rows used), HG = 2 and HG = 1 (one head per kv group), and G = 32 (four
+    8-head q blocks per kv group)."""
     monkeypatch.setenv("GROUT_FMHA_PREFILL_SHARED", "1" if mode == "shared" else "0")
     monkeypatch.setenv("GROUT_FMHA_PREFILL_PAIRED", "1" if mode.startswith("paired") else "0")
     monkeypatch.setenv("GROUT_FMHA_PREFILL_WAVE_ROWS", "16" if mode.endswith("64") else "32")
