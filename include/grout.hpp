@@ -112,6 +112,7 @@ class Engine {
 
   /* New-session prefill over `tokens`; last-token logits (src/api.rs:86-101). */
   Logits prefill(const std::vector<std::uint32_t>& tokens) {
+    need();
     if (tokens.empty()) throw Error(GROUT_EINVAL, "prefill requires at least one token");
     if (tokens.size() > meta_.max_ctx)
       throw Error(GROUT_EINVAL, "prefill length " + std::to_string(tokens.size()) +
@@ -126,6 +127,7 @@ class Engine {
 
   /* One token into the current session; next-token logits (src/api.rs:103-114). */
   Logits decode(std::uint32_t token) {
+    need();
     Logits l;
     l.values.resize(meta_.vocab_size);
     check(grout_engine_decode(e_, token, l.values.data()), "grout_engine_decode");
@@ -134,6 +136,7 @@ class Engine {
 
   /* One token; the greedy next token from the device argmax (src/api.rs:116-129). */
   std::uint32_t decode_greedy(std::uint32_t token) {
+    need();
     std::uint32_t next = 0;
     check(grout_engine_decode_greedy(e_, token, &next), "grout_engine_decode_greedy");
     return next;
@@ -141,20 +144,33 @@ class Engine {
 
   /* Clears the KV state and ends the session; a failure is also stashed and
    * reported by the next call (src/api.rs:131-146). */
-  void reset() { check(grout_engine_reset(e_), "grout_engine_reset"); }
+  void reset() {
+    need();
+    check(grout_engine_reset(e_), "grout_engine_reset");
+  }
 
   /* A dummy one-token prefill and decode with the first stop token, then a
    * fresh session (src/api.rs:153-162). */
-  void warmup() { check(grout_engine_warmup(e_), "grout_engine_warmup"); }
+  void warmup() {
+    need();
+    check(grout_engine_warmup(e_), "grout_engine_warmup");
+  }
 
   const ModelMeta& meta() const noexcept { return meta_; }
 
   /* Position the next decode writes (the reference's next_pos). */
-  std::size_t position() const { return static_cast<std::size_t>(grout_engine_position(e_)); }
+  std::size_t position() const {
+    need();
+    return static_cast<std::size_t>(grout_engine_position(e_));
+  }
 
   grout_engine* raw() const noexcept { return e_; }
 
  private:
+  void need() const {
+    if (e_ == nullptr) throw Error(GROUT_EINVAL, "engine was moved from");
+  }
+
   grout_engine* e_ = nullptr;
   ModelMeta meta_;
 };
