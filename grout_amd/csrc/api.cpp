@@ -121,7 +121,7 @@ int grout_fmha_prefill_plan(int seq_len, int num_q_heads, int num_kv_heads, int*
              "seq_len=%d outside [1, GROUT_MAX_CTX=%d]", seq_len, GROUT_MAX_CTX);
   const grout::PrefillPlan p = grout::plan_fmha_prefill(seq_len, num_q_heads, num_kv_heads);
   if (form) *form = p.shared ? 0 : p.wave_rows == 32 ? 1 : 2;
-  if (paired) *paired = p.shared ? 1 : p.paired;
+  if (paired) *paired = p.paired;
   if (workgroups) *workgroups = p.workgroups;
   return GROUT_OK;
 }

@@ -609,9 +609,10 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
 // the K tiles and team B the V tiles (4 loads per wave per S phase instead of
 // 8), into three K and three V slots (96 KiB).  A workgroup runs the
 // complementary blocks h = nqb2-1-r and l = r back to back (their tile counts
-// add up to a constant), both teams switching from h to l at the same tile;
-// each team writes its own rows, so there is no end-of-kernel merge.  Used
-// when such pairs still give every CU a workgroup.
+// add up to a constant), both teams switching from h to l at the same tile,
+// or (paired = 0) the single block h, heaviest first; each team writes its
+// own rows, so there is no end-of-kernel merge.  Used for long prompts, see
+// plan_fmha_prefill.
 //
 // Slot schedule (team B one phase behind team A; phases counted from 0):
 // G(j) = P(j).V(j) + S(j+1) = Q.K(j+1)^T runs at phase 2j+2 (A) / 2j+3 (B),
@@ -625,7 +626,7 @@ template <int HG>
 __global__ __launch_bounds__(512, 1) void fmha_prefill_shared_kernel(
     const half_t* __restrict__ q, const half_t* __restrict__ k_cache,
     const half_t* __restrict__ v_cache, half_t* __restrict__ out, int S, int pos0, int Hq,
-    int Hkv, long head_stride, float scale_log2, int nqb2) {
+    int Hkv, long head_stride, float scale_log2, int nqb2, int paired) {
   constexpr int BQ = kRowsPerTeam / HG;  // query positions per team
   constexpr int BQ2 = 2 * BQ;           // per block
   __shared__ __attribute__((aligned(1024))) unsigned char s_k0[kTileBytes];
@@ -655,7 +656,9 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_shared_kernel(
     const int q_last = min(qb * BQ2 + BQ2, S) - 1;
     return (pos0 + q_last + 1 + kBN - 1) / kBN;
   };
-  const int h = nqb2 - 1 - r, l = r;
+  // paired: complementary blocks h and l back to back; else one block per
+  // workgroup, heaviest first
+  const int h = nqb2 - 1 - r, l = paired ? r : h;
   const int th = tiles_of(h), tl = l < h ? tiles_of(l) : 0;
   const int n = th + tl;
   auto tile_at = [&](int j) __attribute__((always_inline)) { return j < th ? j : j - th; };
@@ -982,8 +985,8 @@ PrefillPlan plan_fmha_prefill(int seq_len, int Hq, int Hkv) {
   // blocks, heaviest first, which the dispatcher balances like a longest-first
   // list schedule: 128-row blocks when there are at least 192 of them, else
   // 64-row blocks.  Measured over S = 256-8192 at G = 4 and 8 (Qwen3-4B and
-  // -32B heads): the pick is the fastest form or within 2% of it at every
-  // length.
+  // -32B heads): the pick is the fastest of the six forms or within 2% of it
+  // at every length.
   constexpr long kCUs = 256;
   auto fills = [&](long wgs) {
     if (wgs <= kCUs) return 4 * wgs >= 3 * kCUs;
@@ -1007,9 +1010,15 @@ PrefillPlan plan_fmha_prefill(int seq_len, int Hq, int Hkv) {
     p.wave_rows = o;
   const int BQr = p.wave_rows == 32 ? BQ : BQ64;
   p.nqb = (seq_len + BQr - 1) / BQr;
-  p.paired = pairs_fill(p.wave_rows);
+  // The shared stream's pairs take the whole GPU only in full rounds; with
+  // 192-255 of them (one partial round) its single blocks, heaviest first,
+  // finish sooner (measured 3-10%).
+  p.paired = p.shared ? (pairs_of(2 * BQ) >= kCUs ? 1 : 0) : pairs_fill(p.wave_rows);
   if (const int o = env_override("GROUT_FMHA_PREFILL_PAIRED"); o == 0 || o == 1) p.paired = o;
-  p.workgroups = p.shared ? pairs_of(2 * BQ) : (p.paired ? (p.nqb + 1) / 2 : p.nqb) * (long)per_block;
+  if (p.shared)
+    p.workgroups = p.paired ? pairs_of(2 * BQ) : blocks_of(2 * BQ);
+  else
+    p.workgroups = (p.paired ? (p.nqb + 1) / 2 : p.nqb) * (long)per_block;
   return p;
 }
 
@@ -1027,7 +1036,7 @@ hipError_t launch_fmha_prefill(const void* q, const void* k_cache, const void* v
     if (shared)                                                                            \
       fmha_prefill_shared_kernel<hg><<<(unsigned)blocks, 512, 0, stream>>>(                \
           (const half_t*)q, (const half_t*)k_cache, (const half_t*)v_cache, (half_t*)out,  \
-          seq_len, pos0, Hq, Hkv, head_stride, scale_log2, nqb2);                          \
+          seq_len, pos0, Hq, Hkv, head_stride, scale_log2, nqb2, paired);                  \
     else if (wave_rows == 32)                                                              \
       fmha_prefill_kernel<hg, 2><<<(unsigned)blocks, 512, 0, stream>>>(                    \
           (const half_t*)q, (const half_t*)k_cache, (const half_t*)v_cache, (half_t*)out,  \

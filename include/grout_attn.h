@@ -109,10 +109,9 @@ int grout_fmha_prefill(const void* q, const void* k_cache, const void* v_cache, 
 
 /* The work split grout_fmha_prefill launches for seq_len query rows (host
  * only, no GPU; the GROUT_FMHA_PREFILL_SHARED / _PAIRED / _WAVE_ROWS test
- * overrides apply): *form = 0 the shared K/V stream (256-row q blocks in
- * complementary pairs), 1 the per-team kernel with 128-row q blocks, 2 with
- * 64-row q blocks; *paired = 1 for complementary block pairs, 0 for single
- * blocks; *workgroups = the grid size.  Any output pointer may be NULL;
+ * overrides apply): *form = 0 the shared K/V stream (256-row q blocks), 1 the
+ * per-team kernel with 128-row q blocks, 2 with 64-row q blocks; *paired = 1
+ * for complementary block pairs, 0 for single blocks (heaviest first); *workgroups = the grid size.  Any output pointer may be NULL;
  * 1 <= seq_len <= GROUT_MAX_CTX.
  * Stands in for the tile and kernel choice of
  * attend_seq_arc_into_ctx_with_position (src/model.rs:6905-6927, 6946-7079). */

@@ -193,16 +193,16 @@ def test_argument_validation_without_gpu():
 
 
 # Qwen3-4B (32 / 8 heads) and Qwen3-32B (64 / 8): the pick at each length, the
-# fastest of the five forms in a sweep on MI355X (form 0 shared stream, 1 per-team
+# fastest of the six forms in a sweep on MI355X (form 0 shared stream, 1 per-team
 # 128-row blocks, 2 per-team 64-row blocks; paired; workgroups).
 PREFILL_PLANS = {
     (256, 32): (2, 0, 128), (512, 32): (2, 0, 256), (768, 32): (2, 1, 192),
     (1024, 32): (2, 1, 256), (1280, 32): (1, 0, 320), (1536, 32): (1, 1, 192),
-    (2048, 32): (1, 1, 256), (2560, 32): (1, 0, 640), (3072, 32): (0, 1, 192),
+    (2048, 32): (1, 1, 256), (2560, 32): (1, 0, 640), (3072, 32): (0, 0, 384),
     (4096, 32): (0, 1, 256), (5120, 32): (1, 0, 1280), (6144, 32): (1, 1, 768),
     (8192, 32): (0, 1, 512),
     (256, 64): (2, 0, 256), (512, 64): (2, 1, 256), (768, 64): (1, 1, 192),
-    (1024, 64): (1, 1, 256), (1536, 64): (0, 1, 192), (2048, 64): (0, 1, 256),
+    (1024, 64): (1, 1, 256), (1536, 64): (0, 0, 384), (2048, 64): (0, 1, 256),
     (3072, 64): (1, 1, 768), (4096, 64): (0, 1, 512),
 }
 

@@ -350,7 +350,8 @@ def test_prefill_random_shapes_vs_oracle(gpu, monkeypatch, form, S, Hq, Hkv, pos
     assert_close(host_f32(out), ref, f"prefill S={S} Hq={Hq} Hkv={Hkv} pos0={pos0}")
 
 
-@pytest.mark.parametrize("mode", ["single", "paired", "single64", "paired64", "shared"])
+@pytest.mark.parametrize("mode", ["single", "paired", "single64", "paired64", "shared",
+                                  "shared_single"])
 @pytest.mark.parametrize("S,Hq,Hkv,pos0", [
     (1, 32, 8, 0), (17, 32, 8, 0), (130, 64, 8, 0), (200, 32, 8, 77), (77, 40, 8, 9),
     (33, 16, 1, 0), (700, 32, 8, 100), (1000, 16, 4, 0), (2048, 24, 8, 0), (600, 56, 8, 7),
@@ -362,13 +363,15 @@ def test_prefill_work_splits_vs_oracle(gpu, monkeypatch, mode, S, Hq, Hkv, pos0)
     or complementary q-block pairs (team B taking the light block and the
     tail of the heavy one), each with 128-row blocks (32 rows per wave) or
     64-row blocks (16 rows per wave), and the shared K/V stream (256-row
-    blocks, both teams on one staged tile stream, pairs run back to back).
+    blocks, both teams on one staged tile stream, pairs run back to back or
+    one block per workgroup).
     Odd block counts, a kv prefix (pos0 > 0), a single kv head, HG = 3 (rows
     that fall outside a 126- or 63-row block), HG = 5, 6 and 7 (60-63 of 64
     rows used), HG = 2 and HG = 1 (one head per kv group), and G = 32 (four
     8-head q blocks per kv group)."""
-    monkeypatch.setenv("GROUT_FMHA_PREFILL_SHARED", "1" if mode == "shared" else "0")
-    monkeypatch.setenv("GROUT_FMHA_PREFILL_PAIRED", "1" if mode.startswith("paired") else "0")
+    monkeypatch.setenv("GROUT_FMHA_PREFILL_SHARED", "1" if mode.startswith("shared") else "0")
+    monkeypatch.setenv("GROUT_FMHA_PREFILL_PAIRED",
+                       "1" if mode.startswith("paired") or mode == "shared" else "0")
     monkeypatch.setenv("GROUT_FMHA_PREFILL_WAVE_ROWS", "16" if mode.endswith("64") else "32")
     _say("prefill_split", mode, S, Hq, Hkv, pos0)
     max_ctx = pos0 + S + 3
