@@ -14,7 +14,8 @@ Parity pinning (what checks each function independently of its own formula):
 * ``f2h`` / ``h2f``: exhaustive round trip over all 65536 half patterns and
   agreement with numpy's float32 -> float16 cast on random and tie inputs.
 * ``rope_table``: numpy float64 recomputation, cos^2+sin^2=1, position 0 is the
-  identity.
+  identity; ``rope_rows``: equal to the table's rows, and numpy float64 at the
+  last rows of a 2^22-position cache.
 * ``qk_norm_rope_row``: torch ``rms_norm`` + complex-multiplication RoPE in
   float64 (within f16 rounding), RMSNorm scale invariance, RoPE norm
   preservation and relative-position property.

@@ -11,7 +11,8 @@
  *
  *   go_inv_freq            src/model.rs:7295-7306   (build_inv_freq)
  *   go_rope_table          src/kernels.rs:5076-5082 (theta = pos*inv_freq; cos/sin),
- *                          src/kernels.rs:1768-1786 (NeoX half-split layout)
+ *                          src/kernels.rs:1768-1786 (NeoX half-split layout);
+ *                          go_rope_rows: a row range of the same table
  *   go_qk_norm_rope_row    src/kernels.rs:4999-5088 (x*rsqrt(ss/D+eps)*gamma, rotate)
  *   go_qk_norm_rope_kv_prefill  src/kernels.rs:4837-5168
  *   go_qk_norm_rope_kv_decode   src/kernels.rs:5170-5452
@@ -39,7 +40,11 @@
  *   - decode qk_scale is 1/sqrt(D) in fp32 (the reference rounds it to f16,
  *     src/model.rs:3725);
  *   - split partials stay fp32 (the reference rounds them to f16,
- *     src/kernels.rs:4176-4179), and P is not rounded to f16 before P.V.
+ *     src/kernels.rs:4176-4179), and P is not rounded to f16 before P.V;
+ *   - go_attention_prefill_rows / go_attention_decode accumulate the softmax
+ *     denominator and P.V in fp64 (scores and exponentials stay fp32), so
+ *     the checker stays exact to well inside the tolerance at 2^22 cached
+ *     positions, where sequential fp32 sums drift by percents.
  */
 #include <math.h>
 #include <pthread.h>
@@ -162,21 +167,27 @@ void go_inv_freq(int D, float theta, float* inv_freq) {
   }
 }
 
-/* cos/sin[pos][i] of the f32 angle (float)pos * inv_freq[i] (src/kernels.rs:5076-5082),
- * evaluated in double and rounded once to f32. Layout [max_ctx][D/2]. */
-void go_rope_table(int max_ctx, int D, float theta, float* cos_t, float* sin_t) {
+/* Rows p0 .. p0+n-1 of the table below, stored from cos_rows[0] / sin_rows[0]
+ * (layout [n][D/2]). */
+void go_rope_rows(int p0, int n, int D, float theta, float* cos_rows, float* sin_rows) {
   int half = D / 2;
   float* inv = (float*)malloc(sizeof(float) * (size_t)half);
   go_inv_freq(D, theta, inv);
-  for (int p = 0; p < max_ctx; ++p) {
-    float pf = (float)p;
+  for (int r = 0; r < n; ++r) {
+    float pf = (float)(p0 + r);
     for (int i = 0; i < half; ++i) {
       float ang = pf * inv[i];
-      cos_t[(size_t)p * half + i] = (float)cos((double)ang);
-      sin_t[(size_t)p * half + i] = (float)sin((double)ang);
+      cos_rows[(size_t)r * half + i] = (float)cos((double)ang);
+      sin_rows[(size_t)r * half + i] = (float)sin((double)ang);
     }
   }
   free(inv);
+}
+
+/* cos/sin[pos][i] of the f32 angle (float)pos * inv_freq[i] (src/kernels.rs:5076-5082),
+ * evaluated in double and rounded once to f32. Layout [max_ctx][D/2]. */
+void go_rope_table(int max_ctx, int D, float theta, float* cos_t, float* sin_t) {
+  go_rope_rows(0, max_ctx, D, theta, cos_t, sin_t);
 }
 
 /* ------------------------------------------------------------------ */
@@ -290,8 +301,13 @@ void go_qk_norm_rope_kv_decode(const uint16_t* qkv, const uint16_t* gamma_q,
 
 /* One query row against kv positions [0, n_kv): fp32 scores, exact softmax
  * (max-subtracted expf), fp32 output.  Loop order of attention_microbench.rs:665-702. */
+/* Scores and exponentials in fp32; the softmax denominator and the weighted
+ * sum of V rows accumulate in fp64.  (An fp32 running sum of millions of
+ * terms drifts: at 2^22 cached positions with one dominant key, each
+ * background term is ~1e-7 of the sum, about one fp32 ulp of it, and the
+ * sequential fp32 sums came out up to 2.7% off a float64 evaluation.) */
 static void go_attend_row(const float* qrow, const uint16_t* kh, const uint16_t* vh, int n_kv,
-                          int D, float scale, float* scores, float* out) {
+                          int D, float scale, float* scores, double* acc, float* out) {
   float mx = -INFINITY;
   for (int n = 0; n < n_kv; ++n) {
     const uint16_t* kr = kh + (size_t)n * D;
@@ -301,17 +317,15 @@ static void go_attend_row(const float* qrow, const uint16_t* kh, const uint16_t*
     scores[n] = sc;
     if (sc > mx) mx = sc;
   }
-  float den = 0.0f;
+  double den = 0.0;
+  for (int d = 0; d < D; ++d) acc[d] = 0.0;
   for (int n = 0; n < n_kv; ++n) {
-    scores[n] = expf(scores[n] - mx);
-    den += scores[n];
-  }
-  for (int d = 0; d < D; ++d) out[d] = 0.0f;
-  for (int n = 0; n < n_kv; ++n) {
-    float w = scores[n] / den;
+    const float p = expf(scores[n] - mx);
+    den += p;
     const uint16_t* vr = vh + (size_t)n * D;
-    for (int d = 0; d < D; ++d) out[d] += w * go_h2f(vr[d]);
+    for (int d = 0; d < D; ++d) acc[d] += (double)p * go_h2f(vr[d]);
   }
+  for (int d = 0; d < D; ++d) out[d] = (float)(acc[d] / den);
 }
 
 /* Causal GQA prefill for selected rows: q[S][Hq][D] (post-RoPE), caches
@@ -330,6 +344,7 @@ static void* go_prefill_worker(void* arg) {
   go_prefill_job* j = (go_prefill_job*)arg;
   int G = j->Hq / j->Hkv, D = j->D;
   float* qrow = (float*)malloc(sizeof(float) * (size_t)D);
+  double* acc = (double*)malloc(sizeof(double) * (size_t)D);
   float* scores = (float*)malloc(sizeof(float) * (size_t)(j->pos0 + j->S));
   for (int ri = 0; ri < j->nrows; ++ri) {
     int r = j->rows[ri];
@@ -338,11 +353,12 @@ static void* go_prefill_worker(void* arg) {
       for (int d = 0; d < D; ++d) qrow[d] = go_h2f(qs[d]);
       int kvh = h / G;
       go_attend_row(qrow, j->kc + (size_t)kvh * j->hs, j->vc + (size_t)kvh * j->hs,
-                    j->pos0 + r + 1, D, j->scale, scores,
+                    j->pos0 + r + 1, D, j->scale, scores, acc,
                     j->out + ((size_t)ri * j->Hq + h) * D);
     }
   }
   free(qrow);
+  free(acc);
   free(scores);
   return NULL;
 }

@@ -10,7 +10,7 @@ import numpy as np
 
 __all__ = [
     "lib", "build", "h2f", "f2h", "fill_normal_f16", "fill_uniform_f16", "fill_normal_f64",
-    "splitmix64_at", "inv_freq", "rope_table", "rsqrt_det", "sumsq_row128",
+    "splitmix64_at", "inv_freq", "rope_table", "rope_rows", "rsqrt_det", "sumsq_row128",
     "qk_norm_rope_row", "qk_norm_rope_kv_prefill", "qk_norm_rope_kv_decode",
     "attention_prefill_rows", "attention_decode", "decode_split", "splitk_merge",
     "Q8_0", "Q4_K", "Q5_K", "Q6_K", "qblock", "dequant", "gemv_q",
@@ -57,6 +57,7 @@ _SIGS = {
     "go_fill_uniform_f16": (None, [_u64, _d, _d, _sz, _u16p]),
     "go_inv_freq": (None, [_i, _f, _f32p]),
     "go_rope_table": (None, [_i, _i, _f, _f32p, _f32p]),
+    "go_rope_rows": (None, [_i, _i, _i, _f, _f32p, _f32p]),
     "go_rsqrt_det": (_f, [_f]),
     "go_sumsq_row128": (_f, [_u16p]),
     "go_qk_norm_rope_row": (None, [_u16p, _u16p, _f32p, _f32p, _f, _u16p]),
@@ -142,6 +143,14 @@ def rope_table(max_ctx: int, D: int, theta: float):
     c = np.empty((max_ctx, D // 2), np.float32)
     s = np.empty((max_ctx, D // 2), np.float32)
     lib().go_rope_table(max_ctx, D, theta, c, s)
+    return c, s
+
+
+def rope_rows(p0: int, n: int, D: int, theta: float):
+    """Rows p0 .. p0+n-1 of rope_table (for caches too long to tabulate whole)."""
+    c = np.empty((n, D // 2), np.float32)
+    s = np.empty((n, D // 2), np.float32)
+    lib().go_rope_rows(p0, n, D, theta, c, s)
     return c, s
 
 

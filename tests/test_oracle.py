@@ -80,6 +80,21 @@ def test_inv_freq_and_rope_table_vs_numpy_float64():
     assert np.max(np.abs(c.astype(np.float64) ** 2 + s.astype(np.float64) ** 2 - 1)) < 3e-7
 
 
+def test_rope_rows_equal_the_table_and_float64_at_the_largest_cache():
+    """rope_rows(p0, n) is rows p0.. of rope_table, bit for bit, and at the
+    last rows of a 2^22-position cache still cos/sin of the f32 angle."""
+    theta = 1e6
+    c, s = O.rope_table(3000, D, theta)
+    for p0, n in ((0, 1), (0, 3000), (1, 7), (2047, 100), (2999, 1)):
+        cr, sr = O.rope_rows(p0, n, D, theta)
+        assert np.array_equal(cr, c[p0:p0 + n]) and np.array_equal(sr, s[p0:p0 + n]), (p0, n)
+    top = (1 << 22) - 64
+    cr, sr = O.rope_rows(top, 64, D, theta)
+    ang = np.arange(top, top + 64).astype(np.float32)[:, None] * O.inv_freq(D, theta)[None, :]
+    assert np.max(np.abs(cr - np.cos(ang.astype(np.float64)))) < 1e-7
+    assert np.max(np.abs(sr - np.sin(ang.astype(np.float64)))) < 1e-7
+
+
 # --------------------------------------------------------- QK-RMSNorm + RoPE
 
 
@@ -241,6 +256,27 @@ def test_decode_vs_torch_and_closed_forms():
     qj = O.f2h(np.repeat(kc[:, j].view(np.float16).astype(np.float32), Hq // Hkv, 0) * 8.0)
     got = O.attention_decode(qj, kc, vc, pos)
     assert np.max(np.abs(got - np.repeat(vc[:, j].view(np.float16).astype(np.float32), Hq // Hkv, 0))) < 1e-3
+
+
+def test_decode_long_context_dominant_key_vs_float64():
+    """2^19 cached positions, one key 16 units of score above an N(0,1)
+    background placed first: every background weight is then ~1e-7 of the
+    softmax sum, about one fp32 ulp of it, where sequential fp32 sums lose
+    percents.  The oracle must still match a float64 softmax."""
+    n, Hq = 1 << 19, 2
+    g = torch.Generator().manual_seed(5)
+    k = torch.randn((1, n, D), generator=g).half()
+    v = torch.randn((1, n, D), generator=g).half()
+    qf = torch.randn((Hq, D), generator=g, dtype=torch.float64)
+    qf = qf / qf.norm(dim=1, keepdim=True) * math.sqrt(D)
+    q = qf.half()
+    k[0, 0] = (q[0].double() / math.sqrt(D) * 16.0).half()  # score 16 for head 0
+    v[0, 0] = (4.0 * torch.randn(D, generator=g)).half()
+    ours = O.attention_decode(q.numpy().view(np.uint16), k.numpy().view(np.uint16),
+                              v.numpy().view(np.uint16), n - 1, nthreads=2)
+    s = (k[0].double() @ q.double().T) / math.sqrt(D)
+    ref = (torch.softmax(s, 0).T @ v[0].double()).numpy()
+    assert np.max(np.abs(ours - ref)) < 1e-4
 
 
 def test_gqa_equals_mha_with_repeated_kv():
