@@ -29,10 +29,12 @@
 //    accumulator layout as is, so each query head stays in one lane column
 //    and its online-softmax statistics live in the lanes that own its
 //    accumulator; the accumulator rescale is skipped unless some head's max
-//    grows by more than 2^8 (lazy rescale);
+//    grows by more than 2^8 (lazy rescale; p = 2^(s - m) against m = the max
+//    minus kPHeadroom then stays below 2^15, inside fp16);
 //  * the 4 waves merge through LDS at the end (float4 per (d block, lane),
 //    conflict-free, one barrier) and write one fp32 partial (unnormalized
-//    acc, max, sum) per (kv head, split, query head); a small second kernel
+//    acc, reference point m, sum of 2^(s - m)) per (kv head, split, query
+//    head); a small second kernel
 //    merges the splits.  (Merging in the last workgroup of each
 //    kv head behind an atomic ticket measured slower on MI355X, also with
 //    every split of a kv head on one XCD so that the partials are L2 hits and
@@ -264,7 +266,7 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES <= 4 ? 2 : 1)) void attn_decode_
                   ((e & 1) << 3);
   }
 
-  float m = -1.0e30f;  // running max (log2 units) of head `col`
+  float m = -1.0e30f;  // reference point (log2 units) of head `col`: its running max - kPHeadroom
   float l = 0.f;       // this lane's part of its sum of p (4 positions per tile)
   floatx4 acc[8];      // O^T: d = 16db + 4kb + i, head col
 #pragma unroll
@@ -286,8 +288,8 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES <= 4 ? 2 : 1)) void attn_decode_
     }
     tmax = fmaxf(tmax, shfl_xor(tmax, 16));
     tmax = fmaxf(tmax, shfl_xor(tmax, 32));
-    if (__any(tmax > m + kDecRescaleThreshold)) {
-      const float mn = fmaxf(m, tmax);
+    if (__any(tmax > m + (kDecRescaleThreshold + kPHeadroom))) {
+      const float mn = fmaxf(m, tmax - kPHeadroom);
       const float alpha = fast_exp2(m - mn);
       m = mn;
       l *= alpha;

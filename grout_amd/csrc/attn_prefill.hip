@@ -60,9 +60,10 @@
 namespace grout {
 
 constexpr int kBN = 64;  // kv positions per tile
-// A lane's share of a tile row sum at or above this sends the tile down the
-// exact-max path of the speculative softmax (see s_phase).
-constexpr float kSpecLimit = 256.0f;
+// A lane's share of a tile row sum at or above this, 2^(8 + kPHeadroom),
+// sends the tile down the exact-max path of the speculative softmax (see
+// s_phase).
+constexpr float kSpecLimit = 32768.0f;
 constexpr int kRowsPerTeam = 128;
 constexpr int kRowBytes = kHeadDim * 2;     // 256 B: one K or V row
 constexpr int kTileBytes = kBN * kRowBytes;  // 16 KiB: one K or V tile
@@ -211,10 +212,11 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
     }
   };
 
-  // m: running max (log2 units) of row `col`; lsum: this lane's share of its
-  // sum of p (the lane group kb covers 16 of every 64 positions); acc: O^T
-  // fragments.  m starts finite and masked scores are -inf, so a row whose
-  // tiles so far are all masked keeps p = 0 (exp2(-inf)) instead of exp2(0).
+  // m: reference point (log2 units) of row `col`, its running max minus
+  // kPHeadroom; lsum: this lane's share of its sum of p = 2^(s - m) (the lane
+  // group kb covers 16 of every 64 positions); acc: O^T fragments.  m starts
+  // finite and masked scores are -inf, so a row whose tiles so far are all
+  // masked keeps p = 0 (exp2(-inf)) instead of exp2(0).
   float m[MB], lsum[MB];
   floatx4 acc[MB][8];
   auto reset_state = [&]() __attribute__((always_inline)) {
@@ -405,11 +407,12 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
             if (16 * pb + i > lim) sc[mb][pb][i] = -__builtin_inff();
       }
     }
-    // Speculative softmax: P against the running max m as it stands, and
-    // this lane's share of each row sum (16 scores).  A share of 2^8 or more
-    // (a score at least ~8 above m, an overflow to inf, or m still at its
-    // initial -1e30) sends the wave to the exact path: tile row max, rescale
-    // of what was accumulated, P again.  Accepted tiles keep p <= 2^8.
+    // Speculative softmax: P against the reference point m as it stands, and
+    // this lane's share of each row sum (16 scores).  A share of kSpecLimit
+    // or more (a score ~8 or more above the running max, an overflow to inf,
+    // or m still at its initial -1e30) sends the wave to the exact path: tile
+    // row max, rescale of what was accumulated, P again.  Accepted tiles keep
+    // p < 2^15.
     float ts[MB];
     auto probs = [&]() __attribute__((always_inline)) {
       const half2v ones = {(half_t)1.f, (half_t)1.f};
@@ -445,7 +448,9 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
         for (int pb = 0; pb < 4; ++pb)
 #pragma unroll
           for (int i = (pb == 0 ? 2 : 0); i < 4; ++i) t = fmaxf(t, sc[mb][pb][i]);
-        const float mnew = fmaxf(m[mb], col_max(t) * scale_log2);
+        // (m + kPHeadroom is the running max; this form needs no register
+        // for the constant)
+        const float mnew = fmaxf(m[mb] + kPHeadroom, col_max(t) * scale_log2) - kPHeadroom;
         const float alpha = fast_exp2(m[mb] - mnew);
         m[mb] = mnew;
         lsum[mb] *= alpha;
@@ -872,7 +877,9 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_shared_kernel(
         for (int pb = 0; pb < 4; ++pb)
 #pragma unroll
           for (int i = (pb == 0 ? 2 : 0); i < 4; ++i) t = fmaxf(t, sc[mb][pb][i]);
-        const float mnew = fmaxf(m[mb], col_max(t) * scale_log2);
+        // (m + kPHeadroom is the running max; this form needs no register
+        // for the constant)
+        const float mnew = fmaxf(m[mb] + kPHeadroom, col_max(t) * scale_log2) - kPHeadroom;
         const float alpha = fast_exp2(m[mb] - mnew);
         m[mb] = mnew;
         lsum[mb] *= alpha;

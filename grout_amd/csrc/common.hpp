@@ -39,6 +39,19 @@ __device__ __forceinline__ u32x4 load16(const void* p) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Headroom (log2 units) of the fp16 probabilities that feed P.V.  The
+// attention kernels form p = 2^(s - m) against m = running max - kPHeadroom
+// rather than the max itself.  Then a tile whose p stay below
+// 2^(8 + kPHeadroom) = 2^15 fits fp16 (65504 at most), and a weight down to
+// 2^-31 of the largest still lands in fp16's range (subnormals reach 2^-24).
+// Against the max itself, the weights below 2^-25 round to zero: with one key
+// ~26 units above a long N(0,1) background, fp16 rounding drops ~27% of the
+// background's mass, and none up to ~30 units with the headroom.  The factor
+// 2^kPHeadroom is in every l and acc alike, so it cancels in acc / l and in
+// the merges, which take (m, l) as a reference point and the sum of
+// 2^(s - m).
+constexpr float kPHeadroom = 7.0f;
+
 // Cross-lane xor shuffle within the wave (ds_bpermute based).
 __device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
 

@@ -129,7 +129,7 @@ int grout_fmha_prefill_plan(int seq_len, int num_q_heads, int num_kv_heads, int*
 int grout_attn_decode_default_splits(int ctx_len, int num_q_heads, int num_kv_heads);
 
 /* Bytes of fp32 scratch grout_attn_decode needs for num_splits splits:
- * partial accumulators [Hkv][splits][G][128] + (max, sum) [Hkv][splits][G][2].
+ * partial accumulators [Hkv][splits][G][128] + (m, sum) [Hkv][splits][G][2].
  * Calls sharing one workspace must not overlap in time. */
 size_t grout_attn_decode_workspace_bytes(int num_q_heads, int num_kv_heads, int head_dim,
                                          int num_splits);
@@ -169,7 +169,8 @@ int grout_attn_decode_noalloc(const void* q, const void* k_cache, const void* v_
 /* The two halves of grout_attn_decode, for callers that schedule them
  * separately (the reference records them as two kernels).  part_acc
  * [Hkv][splits][G][128] fp32 unnormalized, part_ml [Hkv][splits][G][2] fp32
- * (running max in log2 units, sum of 2^(s - max)). */
+ * (reference point m in log2 units, the split's running max minus 7, and
+ * the sum of 2^(s - m); the merge needs only that m and that sum agree). */
 int grout_fmha_decode_gqa_split(const void* q, const void* k_cache, const void* v_cache,
                                 float* part_acc, float* part_ml, const uint32_t* d_pos,
                                 int num_q_heads, int num_kv_heads, int head_dim, int max_ctx,
