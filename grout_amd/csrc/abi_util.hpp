@@ -78,7 +78,7 @@ inline int check_stride(long kv_head_stride, long min_rows) {
 }
 
 constexpr int kMaxDecodeGroup = 16;
-constexpr int kMaxSplits = 4096;
+constexpr int kMaxSplits = GROUT_MAX_SPLITS;
 
 // Workspace layout: part_acc [Hkv][splits][G][128] f32 | part_ml [Hkv][splits][G][2] f32.
 inline size_t decode_ws_bytes(int hq, int hkv, int nsplit) {

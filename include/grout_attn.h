@@ -39,6 +39,9 @@ extern "C" {
  * 32-bit byte offsets. */
 #define GROUT_MAX_CTX (1 << 22)
 
+/* Largest decode split count (num_splits) any entry point accepts. */
+#define GROUT_MAX_SPLITS 4096
+
 /* Message of the last failing call on this thread ("" if none). */
 const char* grout_last_error(void);
 
@@ -137,7 +140,8 @@ size_t grout_attn_decode_workspace_bytes(int num_q_heads, int num_kv_heads, int 
 /* q [Hq][128] post-RoPE (q head h = kvh*G + g, i.e. the [Hkv][G][128] grouped
  * view), caches [Hkv][..][128], out [Hq][128].  Attends to positions
  * 0 .. d_pos[0] (s_kv = d_pos[0]+1, clamped to max_ctx).  num_splits <= 0
- * picks grout_attn_decode_default_splits(max_ctx, ...).  Two launches
+ * picks grout_attn_decode_default_splits(max_ctx, ...); at most
+ * GROUT_MAX_SPLITS, and splits past the context's tiles stay empty.  Two launches
  * (split pass, then the merge) on `stream`.
  * Replaces fmha_decode_gqa_split + splitk_reduce_merge
  * (src/kernels.rs:3996-4304) as recorded in src/model.rs:3713-3771. */

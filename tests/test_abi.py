@@ -190,6 +190,13 @@ def test_argument_validation_without_gpu():
     # NULL position pointer
     rc = L.grout_fmha_decode_gqa_split(p, p, p, p, p, None, 8, 2, 128, 64, 64 * 128, 2, 0.088, None)
     assert rc == -1 and "d_pos" in _lib.last_error()
+    # split counts past GROUT_MAX_SPLITS (4096)
+    rc = L.grout_fmha_decode_gqa_split(p, p, p, p, p, p, 8, 2, 128, 64, 64 * 128, 4097, 0.088, None)
+    assert rc == -1 and "4096" in _lib.last_error()
+    rc = L.grout_attn_decode(p, p, p, p, p, 1 << 30, p, 8, 2, 128, 64, 64 * 128, 4097, 0.088, None)
+    assert rc == -1 and "4096" in _lib.last_error()
+    rc = L.grout_splitk_reduce_merge(p, p, p, 8, 2, 128, 4097, None)
+    assert rc == -1 and "4096" in _lib.last_error()
 
 
 # Qwen3-4B (32 / 8 heads) and Qwen3-32B (64 / 8): the pick at each length, the

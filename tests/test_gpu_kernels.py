@@ -95,7 +95,7 @@ def _decode_case(gpu, Hq, Hkv, ctx, max_ctx, num_splits, tag):
     q = normal(tag + "q", (Hq, D))
     kc = normal(tag + "k", (Hkv, max_ctx, D))
     vc = normal(tag + "v", (Hkv, max_ctx, D))
-    ref = O.attention_decode(q, kc, vc, ctx - 1, nthreads=8)
+    ref = O.attention_decode(q, kc, vc, ctx - 1, nthreads=16)
     p = torch.tensor([ctx - 1], dtype=torch.int32, device="cuda")
     out = gpu.ops.attn_decode(dev(q), dev(kc), dev(vc), p, num_splits=num_splits)
     torch.cuda.synchronize()
@@ -117,6 +117,8 @@ def _decode_case(gpu, Hq, Hkv, ctx, max_ctx, num_splits, tag):
     (16, 1, 1500, 2048, None),    # one kv head (G = 16)
     (28, 4, 900, 1024, 5),        # Hkv = 4, G = 7
     (32, 16, 2000, 2048, None),   # Hkv = 16, G = 2
+    (64, 8, 131072, 131072, 4096),  # GROUT_MAX_SPLITS: one 32-position tile per split, G = 8
+    (16, 8, 3000, 4096, 4096),    # GROUT_MAX_SPLITS, 94 tiles: all but 94 splits empty
 ])
 def test_decode_attention_vs_oracle(gpu, Hq, Hkv, ctx, max_ctx, splits):
     _decode_case(gpu, Hq, Hkv, ctx, max_ctx, splits, f"dec{Hq}_{ctx}")
@@ -156,6 +158,7 @@ def test_decode_random_shapes_vs_oracle(gpu, Hq, Hkv, ctx, max_ctx, splits):
     (16, 8, 47, 64, 7),           # more splits than tiles
     (16, 1, 300, 512, None),      # one kv head
     (28, 4, 200, 256, 3),         # Hkv = 4, G = 7
+    (32, 8, 4095, 4096, 4096),    # GROUT_MAX_SPLITS: the new row's split among 4000 empty ones
 ])
 def test_fused_decode_step_vs_oracle(gpu, Hq, Hkv, pos, max_ctx, splits):
     """Norm/RoPE/KV write fused into the decode attention: cache rows
