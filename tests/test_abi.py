@@ -138,6 +138,21 @@ def test_integration_rust_block_declares_every_header_function():
     assert declared == set(header_functions())
 
 
+def test_integration_rust_constants_match_the_headers():
+    """Every value #define of both headers appears in the Rust block as a
+    `pub const` of the same value (status codes, limits, weight formats)."""
+    defines = {}
+    for h in ("grout_attn.h", "grout_engine.h"):
+        for name, val in re.findall(r"^#define (GROUT_[A-Z0-9_]+) +([^/\n]+)",
+                                    open(os.path.join(ROOT, "include", h)).read(), re.M):
+            defines[name] = eval(val.strip())  # integer literals, shifts, negation
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    block = text[text.index("## 1."):text.index("## 2.")]
+    consts = {n: eval(v) for n, v in re.findall(r"pub const (GROUT_[A-Z0-9_]+): \w+ = ([^;]+);",
+                                                block)}
+    assert consts == defines
+
+
 def test_rope_host_functions_match_oracle_bit_for_bit():
     import oracle as O
 
