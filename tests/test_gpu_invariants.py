@@ -9,7 +9,10 @@ softmax attention by construction.
 * q = lambda * k_j with lambda = 8: the weight of position j dominates by
   e^60 or more, so output = v_j for every query that sees j;
 * GQA == MHA with each kv head repeated G times (the kernels' head grouping
-  changes, the math does not).
+  changes, the math does not);
+* the split count of decode changes nothing beyond one f16 ulp;
+* the norm/RoPE kernel: position 0 is the identity, RoPE keeps pair norms and
+  relative positions, RMSNorm ignores an exact 4x scale.
 
 Decode runs with one, several and the default number of splits (and the
 fused norm/RoPE/KV layer for the first two forms, with the cache row it writes
@@ -172,3 +175,54 @@ def test_prefill_gqa_equals_mha(gpu, monkeypatch, form):
     gqa = _prefill(gpu, q, kc, vc, pos0)
     mha = _prefill(gpu, q, np.repeat(kc, G, 0), np.repeat(vc, G, 0), pos0)
     assert np.max(np.abs(gqa - mha)) <= 2e-3 and np.mean(np.abs(gqa - mha)) <= 2e-4
+
+
+def test_decode_split_count_invariance(gpu):
+    """The same decode with 1, 2, 7, 16, 64 and 200 splits (200 > the 47 tiles
+    of 16 positions: empty splits): outputs within one f16 ulp."""
+    Hq, Hkv, max_ctx, pos = 32, 8, 1024, 750
+    q = normal("sq", (Hq, D))
+    kc, vc = normal("sk", (Hkv, max_ctx, D)), normal("sv", (Hkv, max_ctx, D))
+    outs = {n: _decode(gpu, q, kc, vc, pos, n) for n in (1, 2, 7, 16, 64, 200)}
+    for n, o in outs.items():
+        d = np.abs(o - outs[1])
+        # one f16 ulp: the f16 P is rounded against each split's own
+        # reference point, so about half the outputs round the other way
+        assert np.all(d <= 2.0**-10 * np.maximum(np.abs(outs[1]), 2.0**-3)), n
+
+
+def test_norm_rope_invariants_on_the_kernel(gpu):
+    """The fused QK-norm/RoPE prefill kernel on one q row x and one k row y
+    repeated at positions 0..S-1 (gamma = 1): position 0 is the identity
+    (unit RMS after the norm), every (i, i+64) pair keeps its norm at every
+    position, <q(m), k(n)> depends only on m - n, and 4x (exact in f16)
+    changes nothing, bit for bit (with eps = 1e-30: a finite eps next to
+    the mean square would break the exact scale invariance)."""
+    Hq, Hkv, S = 2, 1, 1400
+    x, y = normal("rx", (D,)), normal("ry", (D,))
+    ones = np.full(D, _h(1.0))
+    rope = gpu.ops.rope_tables(S)
+
+    def run(xs, ys):
+        q = np.ascontiguousarray(np.broadcast_to(xs, (S, Hq, D)))
+        k = np.ascontiguousarray(np.broadcast_to(ys, (S, Hkv, D)))
+        kc = torch.zeros((Hkv, S, D), dtype=torch.float16, device="cuda")
+        vc = torch.zeros_like(kc)
+        qo = gpu.ops.qk_norm_rope_kv_prefill(dev(q), dev(k), dev(np.zeros_like(k)), dev(ones),
+                                             dev(ones), rope, kc, vc, 0, eps=1e-30)
+        torch.cuda.synchronize()
+        return host(qo), host(kc)
+
+    qo16, kc16 = run(x, y)
+    qo, ko = _f64(qo16)[:, 0], _f64(kc16)[0]
+    assert abs(np.sqrt(np.mean(qo[0] ** 2)) - 1.0) < 2e-3, "unit RMS at position 0"
+    pair0 = qo[0, :64] ** 2 + qo[0, 64:] ** 2
+    for p in (1, 100, 777, S - 1):
+        pair = qo[p, :64] ** 2 + qo[p, 64:] ** 2
+        assert np.allclose(pair, pair0, rtol=4e-3, atol=2e-4), p
+    d1, d2 = qo[700] @ ko[650], qo[1350] @ ko[1300]
+    assert abs(d1 - d2) < 2e-2 * max(1.0, abs(d1)), (d1, d2)
+    x4 = (_f64(x) * 4.0).astype(np.float16).view(np.uint16)
+    y4 = (_f64(y) * 4.0).astype(np.float16).view(np.uint16)
+    qo4, kc4 = run(x4, y4)
+    assert np.array_equal(qo4, qo16) and np.array_equal(kc4, kc16), "RMSNorm(4x) == RMSNorm(x)"
