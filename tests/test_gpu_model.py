@@ -633,6 +633,38 @@ def test_engine_qwen3_4b_shapes_consistency(gpu):
         torch.cuda.empty_cache()
 
 
+def test_engine_qwen3_4b_long_context_consistency(gpu):
+    """Full Qwen3-4B shapes at Qwen3's whole context (max_position_embeddings
+    40960), random N(0, 0.02) weights: the decode step at position 40959 after
+    a 40959-token prompt equals a prefill of all 40960 tokens (the prefill
+    FMHA at S = 40960 in several rounds of the shared K/V stream; the fused
+    decode over 40960 positions), and so does a 20000-token prefill extended
+    by the other 20960 in one chunk (pos0 = 20000 through the GEMMs, the
+    fused write and the FMHA)."""
+    from grout_amd.model import Engine, Qwen3Config, Qwen3Weights
+
+    cfg = Qwen3Config.qwen3_4b()
+    n, half = 40960, 20000
+    w = Qwen3Weights.random(cfg, seed=0)
+    eng = Engine(cfg, w, max_ctx=n)
+    try:
+        prompt = [int(t) for t in np.random.default_rng(40960).integers(0, cfg.vocab_size, n)]
+        print("4b long context: whole prefill", flush=True)
+        whole = eng.prefill(prompt).values
+        print("4b long context: prefill n-1, decode", flush=True)
+        eng.prefill(prompt[:-1])
+        step = eng.decode(prompt[-1]).values
+        check_logits(step, whole, "4b decode at 40959 vs prefill of 40960")
+        print("4b long context: prefill + extend", flush=True)
+        eng.prefill(prompt[:half])
+        ext = eng.extend(prompt[half:]).values
+        check_logits(ext, whole, "4b prefill 20000 + extend 20960 vs prefill of 40960")
+    finally:
+        eng.close()
+        del w
+        torch.cuda.empty_cache()
+
+
 def test_engine_qwen3_32b_shapes_consistency(gpu):
     """Full Qwen3-32B shapes (64 layers, hidden 5120, MLP 25600, 64/8 heads,
     untied head; 65.5 GB of random N(0, 0.02) fp16 weights): the same
