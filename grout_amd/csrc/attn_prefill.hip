@@ -157,8 +157,9 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
     return (pos0 + q_last + 1 + kBN - 1) / kBN;
   };
   // Work split (workgroup-uniform): blocks h >= l, team A tiles [0, a) of h,
-  // team B tiles [0, tl) of l then [a, th) of h.
-  const int h = paired ? nqb - 1 - r : nqb - 1 - r;
+  // team B tiles [0, tl) of l then [a, th) of h.  Heaviest blocks first in
+  // both forms; unpaired, l = h means no light block.
+  const int h = nqb - 1 - r;
   const int l = paired ? r : h;
   const int th = tiles_of(h), tl = h != l ? tiles_of(l) : 0;
   const int a = (th + tl + 1) / 2;
