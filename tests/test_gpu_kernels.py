@@ -307,7 +307,8 @@ def test_decode_reuses_workspace_across_calls(gpu):
 
 @pytest.mark.parametrize("S,Hq,Hkv,pos0", [
     (1, 32, 8, 0), (17, 32, 8, 0), (64, 16, 8, 3), (200, 32, 8, 77), (130, 64, 8, 0),
-    (96, 8, 8, 10), (77, 40, 8, 9), (33, 16, 1, 0), (150, 48, 8, 5), (111, 56, 8, 0)])
+    (96, 8, 8, 10), (77, 40, 8, 9), (33, 16, 1, 0), (150, 48, 8, 5), (111, 56, 8, 0),
+    (1, 32, 8, 4095), (3, 64, 8, 1000)])  # a one-token extend, a short chunk after a long prefix
 def test_prefill_attention_vs_oracle(gpu, S, Hq, Hkv, pos0):
     _say("prefill", S, Hq, Hkv, pos0)
     max_ctx = pos0 + S + 5
