@@ -194,3 +194,66 @@ def test_tensor_errors(tmp_path):
     p = tmp_path / "short.gguf"
     p.write_bytes(bytes(data[:-1000]))
     _err(p, "outside the file|truncated")
+
+
+_FUZZ_CHILD = r'''
+import ctypes as C, json, struct, sys
+import numpy as np
+sys.path.insert(0, sys.argv[1])
+from grout_amd._lib import ModelInfo, lib
+base, path, n = open(sys.argv[2], "rb").read(), sys.argv[3], int(sys.argv[4])
+L, rng = lib(), np.random.default_rng(2718)
+head = min(len(base), 8192)  # header, metadata and tensor infos live here
+rcs = {}
+for i in range(n):
+    b = bytearray(base)
+    kind = i % 6
+    pos = int(rng.integers(0, head if rng.random() < 0.85 else len(b)))
+    if kind == 0:    # flipped bits
+        for _ in range(int(rng.integers(1, 9))):
+            b[int(rng.integers(0, head))] ^= 1 << int(rng.integers(0, 8))
+    elif kind == 1:  # truncated
+        del b[pos:]
+    elif kind == 2:  # a 64-bit field (length, count, dimension, offset) set to an extreme
+        v = [2**64 - 1, 2**63, 2**62 + 1, 2**32, 2**31 - 1, int(rng.integers(0, 2**63))]
+        b[pos:pos + 8] = struct.pack("<Q", v[int(rng.integers(0, len(v)))])
+    elif kind == 3:  # inserted bytes
+        b[pos:pos] = rng.bytes(int(rng.integers(1, 64)))
+    elif kind == 4:  # dropped bytes
+        del b[pos:pos + int(rng.integers(1, 64))]
+    else:            # a 32-bit field (type, version, dimension count) set to an extreme
+        v = [0, 1, 12, 13, 30, 31, 255, 2**31, 2**32 - 1]
+        b[pos:pos + 4] = struct.pack("<I", v[int(rng.integers(0, len(v)))])
+    with open(path, "wb") as f:
+        f.write(b)
+    info = ModelInfo()
+    rc = L.grout_model_inspect(path.encode(), C.byref(info))
+    if rc != 0 and not L.grout_last_error():
+        print(json.dumps({"case": i, "rc": rc, "error": "no message"}))
+        sys.exit(3)
+    rcs[str(rc)] = rcs.get(str(rc), 0) + 1
+print(json.dumps(rcs))
+'''
+
+
+def test_inspect_survives_corrupted_files(tmp_path):
+    """3000 seeded corruptions of a valid GGUF (flipped bits, truncation,
+    inserted and dropped bytes, 32- and 64-bit fields set to extremes, mostly
+    in the header, metadata and tensor infos), inspected in one child
+    process: every call returns OK or an error status with a message, and
+    nothing crashes or hangs (a crash fails this test with its signal)."""
+    import json
+    import os
+    import subprocess
+    import sys
+
+    _, path = model_file(tmp_path)
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _FUZZ_CHILD, root, str(path),
+                        str(tmp_path / "fuzz.gguf"), "3000"],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, (r.returncode, r.stdout[-2000:], r.stderr[-2000:])
+    rcs = json.loads(r.stdout.strip().splitlines()[-1])
+    assert sum(rcs.values()) == 3000
+    assert set(rcs) <= {"0", "-1", "-3"}, rcs   # OK, EINVAL, ENOTSUP
+    assert rcs.get("-1", 0) > 1000, rcs           # most corruptions are caught
