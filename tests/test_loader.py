@@ -130,3 +130,78 @@ def test_config_json_with_escapes_and_nesting(tmp_path):
                      config_over={"name_or_path": "Qwen\\/é😀 \"x\"\n",
                                   "rope_scaling": {"a": [1, 2.5e-3, {"b": None}], "c": True}})
     assert M.inspect(tmp_path)["config"].hidden_size == 64
+
+
+_FUZZ_CHILD = r'''
+import ctypes as C, json, os, struct, sys
+import numpy as np
+sys.path.insert(0, sys.argv[1])
+from grout_amd._lib import ModelInfo, lib
+d, n = sys.argv[2], int(sys.argv[3])
+names = sorted(os.listdir(d))
+orig = {f: open(os.path.join(d, f), "rb").read() for f in names}
+def span(f, b):  # where the parser reads: JSON files whole, safetensors 8 + header bytes
+    if f.endswith(".safetensors"):
+        return min(len(b), 8 + struct.unpack("<Q", orig[f][:8])[0])
+    return len(b)
+L, rng = lib(), np.random.default_rng(31415)
+rcs = {}
+for i in range(n):
+    f = names[int(rng.integers(0, len(names)))]
+    b = bytearray(orig[f])
+    kind, hi = i % 6, span(f, b)
+    pos = int(rng.integers(0, hi))
+    if kind == 0:    # flipped bits
+        for _ in range(int(rng.integers(1, 9))):
+            b[int(rng.integers(0, hi))] ^= 1 << int(rng.integers(0, 8))
+    elif kind == 1:  # truncated
+        del b[pos:]
+    elif kind == 2:  # inserted JSON punctuation, escapes, digits or random bytes
+        pool = [b"{", b"}", b"[", b"]", b'"', b"\\", b"\\u", b",", b":", b"-", b"1e999",
+                b"18446744073709551616", b"\x00", rng.bytes(int(rng.integers(1, 32)))]
+        b[pos:pos] = pool[int(rng.integers(0, len(pool)))]
+    elif kind == 3:  # dropped bytes
+        del b[pos:pos + int(rng.integers(1, 32))]
+    elif kind == 4:  # the safetensors header length (or any 8 bytes) set to an extreme
+        v = [2**64 - 1, 2**63, 2**32, 0, 7, len(b), int(rng.integers(0, 2**63))]
+        at = 0 if f.endswith(".safetensors") and rng.random() < 0.5 else pos
+        b[at:at + 8] = struct.pack("<Q", v[int(rng.integers(0, len(v)))])
+    else:            # a digit replaced: numbers out of range, negative, huge
+        digits = [j for j in range(hi) if 48 <= b[j] <= 57]
+        if digits:
+            j = digits[int(rng.integers(0, len(digits)))]
+            b[j:j + 1] = [b"9999999999999999999999", b"-1", b"0", b"1.5", b"nan"][int(rng.integers(0, 5))]
+    with open(os.path.join(d, f), "wb") as fh:
+        fh.write(b)
+    info = ModelInfo()
+    rc = L.grout_model_inspect(d.encode(), C.byref(info))
+    if rc != 0 and not L.grout_last_error():
+        print(json.dumps({"case": i, "file": f, "rc": rc, "error": "no message"}))
+        sys.exit(3)
+    rcs[str(rc)] = rcs.get(str(rc), 0) + 1
+    with open(os.path.join(d, f), "wb") as fh:
+        fh.write(orig[f])
+print(json.dumps(rcs))
+'''
+
+
+def test_inspect_survives_corrupted_checkpoints(tmp_path):
+    """3000 seeded corruptions of a two-shard checkpoint (one file per case:
+    config.json, generation_config.json, the shard index or a safetensors
+    header; flipped bits, truncation, inserted JSON punctuation and escapes,
+    dropped bytes, header lengths and numbers set to extremes), inspected in
+    one child process: every call returns OK or an error status with a
+    message, and nothing crashes or hangs."""
+    import subprocess
+    import sys
+
+    write_checkpoint(tmp_path, TINY, dtypes=("BF16", "F32", "F16"), shards=2,
+                     generation_eos=[151645, 151643])
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _FUZZ_CHILD, root, str(tmp_path), "3000"],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, (r.returncode, r.stdout[-2000:], r.stderr[-2000:])
+    rcs = json.loads(r.stdout.strip().splitlines()[-1])
+    assert sum(rcs.values()) == 3000
+    assert set(rcs) <= {"0", "-1", "-3"}, rcs   # OK, EINVAL, ENOTSUP
+    assert rcs.get("-1", 0) > 1000, rcs
