@@ -226,3 +226,28 @@ def test_norm_rope_invariants_on_the_kernel(gpu):
     y4 = (_f64(y) * 4.0).astype(np.float16).view(np.uint16)
     qo4, kc4 = run(x4, y4)
     assert np.array_equal(qo4, qo16) and np.array_equal(kc4, kc16), "RMSNorm(4x) == RMSNorm(x)"
+
+
+def test_repeated_calls_are_bit_identical(gpu, monkeypatch):
+    """No kernel here accumulates with atomics or depends on scheduling:
+    the same inputs give bit-identical outputs on every call, in every
+    prefill work split and decode form (calls interleaved with others)."""
+    S, Hq, Hkv, pos0, max_ctx = 700, 32, 8, 20, 1024
+    q = dev(normal("dq", (S, Hq, D)))
+    kc, vc = dev(normal("dk", (Hkv, max_ctx, D))), dev(normal("dv", (Hkv, max_ctx, D)))
+    outs = {}
+    for rep in range(2):
+        for form in sorted(PREFILL_FORMS):
+            for k in ("GROUT_FMHA_PREFILL_SHARED", "GROUT_FMHA_PREFILL_WAVE_ROWS",
+                      "GROUT_FMHA_PREFILL_PAIRED"):
+                monkeypatch.delenv(k, raising=False)
+            for k, v in PREFILL_FORMS[form].items():
+                monkeypatch.setenv(k, v)
+            outs.setdefault(form, []).append(gpu.ops.fmha_prefill(q, kc, vc, pos0).clone())
+        p = torch.tensor([900], dtype=torch.int32, device="cuda")
+        for n in (1, 7, None):
+            outs.setdefault(f"decode{n}", []).append(
+                gpu.ops.attn_decode(q[0], kc, vc, p, num_splits=n).clone())
+    torch.cuda.synchronize()
+    for name, (a, b) in outs.items():
+        assert torch.equal(a, b), name
