@@ -425,6 +425,21 @@ def bench_engine(prompt_len=512, decode_steps=256, max_ctx=1024, cfg=None):
         toks.append(eng.decode_greedy(toks[-1]))
     decode_s = time.perf_counter() - t0
     eng.close()
+    # whole-prompt prefill at the reference's published lengths, on an engine
+    # with room for the longest (median of 3 after one untimed call each)
+    eng = Engine(cfg, w, max_ctx=max(PREFILL_SWEEP_PP) + 1)
+    pre_sweep = {}
+    for pp in PREFILL_SWEEP_PP:
+        pr = np.random.default_rng(pp).integers(0, cfg.vocab_size, pp)
+        eng.prefill_greedy(pr)
+        ts = []
+        for _ in range(3):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            eng.prefill_greedy(pr)
+            ts.append(time.perf_counter() - t0)
+        pre_sweep[pp] = sorted(ts)[1] * 1e3
+    eng.close()
     # per decode token: every fp16 weight once (the tied embedding is read as
     # the lm_head; the embedding gather is one row, so an untied embedding
     # does not count) + K and V of the live context
@@ -436,7 +451,14 @@ def bench_engine(prompt_len=512, decode_steps=256, max_ctx=1024, cfg=None):
     torch.cuda.empty_cache()
     return dict(prefill_ms=prefill_s * 1e3, decode_ms=decode_s * 1e3 / decode_steps,
                 tok_s=decode_steps / decode_s, bytes_per_token=weight_bytes + kv_bytes,
-                distinct_tokens=len(set(toks)), mean_ctx=mean_ctx)
+                distinct_tokens=len(set(toks)), mean_ctx=mean_ctx, prefill_sweep_ms=pre_sweep)
+
+
+# Reference's published Qwen3-4B fp16 whole-prefill latency, median ms, grout
+# tuned for one RTX 5090 (benchmarks/pytorch/README.md:32-38): other hardware,
+# context for the sweep, not a baseline of this path.
+PREFILL_SWEEP_PP = (18, 128, 512, 2048, 8192)
+REFERENCE_4B_RTX5090_PREFILL_MS = {18: 6.31, 128: 7.39, 512: 14.50, 2048: 50.69, 8192: 279.12}
 
 
 # Reference's published request_gen_tps for Qwen3-32B on one B200
@@ -946,6 +968,13 @@ def main():
                         "256 greedy decode steps (decode-step hipGraph)",
             "decode_tok_s": round(r["tok_s"], 1), "decode_ms_per_token": round(r["decode_ms"], 4),
             "prefill_512_ms": round(r["prefill_ms"], 2),
+            "prefill_sweep": {str(pp): {"ms": round(ms, 2), "tok_s": round(pp / ms * 1e3, 1),
+                                        "reference_rtx5090_ms": REFERENCE_4B_RTX5090_PREFILL_MS[pp]}
+                              for pp, ms in r["prefill_sweep_ms"].items()},
+            "prefill_sweep_context": "whole-prompt prefill (embedding to last-token logits, "
+                                     "median of 3); reference_rtx5090_ms: grout's published "
+                                     "medians on one RTX 5090 (benchmarks/pytorch/README.md:"
+                                     "32-38; other hardware)",
             "weight_stream_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
             "attention_share": round(r["attn_graph_ms"] / r["decode_ms"], 4),
             "attention_us_per_token": round(r["attn_graph_ms"] * 1e3, 1)}
@@ -972,6 +1001,13 @@ def main():
                         "512-token prompt, 256 greedy decode steps (decode-step hipGraph)",
             "decode_tok_s": round(r["tok_s"], 1), "decode_ms_per_token": round(r["decode_ms"], 4),
             "prefill_512_ms": round(r["prefill_ms"], 2),
+            "prefill_sweep": {str(pp): {"ms": round(ms, 2), "tok_s": round(pp / ms * 1e3, 1),
+                                        "reference_rtx5090_ms": REFERENCE_4B_RTX5090_PREFILL_MS[pp]}
+                              for pp, ms in r["prefill_sweep_ms"].items()},
+            "prefill_sweep_context": "whole-prompt prefill (embedding to last-token logits, "
+                                     "median of 3); reference_rtx5090_ms: grout's published "
+                                     "medians on one RTX 5090 (benchmarks/pytorch/README.md:"
+                                     "32-38; other hardware)",
             "weight_bytes": r["weight_bytes"],
             "weight_stream_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
     if ok("engine4b_q5km"):
@@ -983,6 +1019,13 @@ def main():
                         "512-token prompt, 256 greedy decode steps (decode-step hipGraph)",
             "decode_tok_s": round(r["tok_s"], 1), "decode_ms_per_token": round(r["decode_ms"], 4),
             "prefill_512_ms": round(r["prefill_ms"], 2),
+            "prefill_sweep": {str(pp): {"ms": round(ms, 2), "tok_s": round(pp / ms * 1e3, 1),
+                                        "reference_rtx5090_ms": REFERENCE_4B_RTX5090_PREFILL_MS[pp]}
+                              for pp, ms in r["prefill_sweep_ms"].items()},
+            "prefill_sweep_context": "whole-prompt prefill (embedding to last-token logits, "
+                                     "median of 3); reference_rtx5090_ms: grout's published "
+                                     "medians on one RTX 5090 (benchmarks/pytorch/README.md:"
+                                     "32-38; other hardware)",
             "weight_bytes": r["weight_bytes"],
             "weight_stream_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
     # sections that failed carry their error instead of numbers
