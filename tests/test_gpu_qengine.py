@@ -210,3 +210,38 @@ def test_gguf_load_vs_quantized_engine_and_oracle(gpu, tmp_path, plan):
     finally:
         loaded.close()
         direct.close()
+
+
+def test_qengine_qwen3_4b_q4km_shapes_consistency(gpu):
+    """Full Qwen3-4B shapes (36 layers, vocab 151936) over random GGUF-block
+    weights in a Q4_K_M-style mix (attn_v / ffn_down Q6_K in the first and
+    last eighth of the layers and every third between, Q6_K tied embedding):
+    the decode step at position n (low-bit GEMVs on the decode-layout
+    scales) equals a prefill of n + 1 tokens (dequantized f16 weights
+    through the GEMMs) within the engine tolerance, and the device argmax
+    equals the host argmax of the same logits."""
+    import torch
+    from grout_amd.model import Engine, QuantWeights, Qwen3Config
+
+    cfg = Qwen3Config.qwen3_4b()
+    L = cfg.num_layers
+
+    def fmts(l):
+        hi = Q6 if l < L // 8 or l >= 7 * L // 8 or (l - L // 8) % 3 == 2 else Q4
+        return {"q": Q4, "k": Q4, "v": hi, "o": Q4, "gate": Q4, "up": Q4, "down": hi}
+
+    qw = QuantWeights.random(cfg, fmts, embed_fmt=Q6, seed=0)
+    eng = Engine.from_quantized(cfg, qw, max_ctx=1024)
+    try:
+        prompt = [int(t) for t in np.random.default_rng(4).integers(0, cfg.vocab_size, 96)]
+        eng.prefill(prompt)
+        t = 777
+        step = eng.decode(t).values
+        full = eng.prefill(prompt + [t]).values
+        check_logits(step, full, "q4km 4b decode vs prefill")
+        eng.prefill(prompt)
+        assert eng.decode_greedy(t) == int(np.argmax(step))
+    finally:
+        eng.close()
+        del qw
+        torch.cuda.empty_cache()
