@@ -780,87 +780,11 @@ def guarded(fn):
         return {"error": f"{type(ex).__name__}: {ex}"[:400]}
 
 
-def main():
-    a = parse()
-    if a.gpus != 1:
-        print(f"bench.py measures one GPU only: this build has no multi-GPU path "
-              f"(requested --gpus {a.gpus}); run with --gpus 1", file=sys.stderr)
-        return 2
-    import torch
-    import grout_amd
-    from grout_amd import ops
-
-    global GRAPH_TIMING
-    GRAPH_TIMING = not a.eager
-    grout_amd.lib()
-    if a.copy_calib:
-        src = torch.ones(128 << 20, dtype=torch.float16, device="cuda")
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(f"# copy_calib: 3 copies of {src.numel() * 2} bytes", file=sys.stderr, flush=True)
-        del src, dst
-    only = set(filter(None, a.only.split(",")))
-    want = lambda k: not only or k in only
-    res = {}
-    if want("decode32b"):
-        res["decode32b_sweep"] = bench_decode32b_sweep(ops, (8192, 16384, 32768), a.steps,
-                                                       a.warmup)
-        res["decode32b"] = res["decode32b_sweep"][32768]
-        print(f"# decode32b {res['decode32b']}", file=sys.stderr, flush=True)
-    if want("prefill"):
-        sweep = guarded(lambda: {S: bench_prefill(ops, S, 32, 8,
-                                                  max(a.steps // (4 if S < 8192 else 10), 10),
-                                                  a.warmup)
-                                 for S in (512, 2048, 8192)})
-        if "error" in sweep:
-            res["prefill_error"] = sweep
-        else:
-            res["prefill_sweep"] = sweep
-            res["prefill"] = sweep[2048]
-        print(f"# prefill {sweep}", file=sys.stderr, flush=True)
-    if want("decode4b"):
-        def decode4b():
-            r = bench_decode(ops, 32, 8, 4096, 32768, 36, a.steps, a.warmup)
-            r["graph_ms"] = bench_decode_graph(grout_amd, 32, 8, 4096, 32768, 36,
-                                               max(a.steps // 4, 10), a.warmup)
-            return r
-        res["decode4b"] = guarded(decode4b)
-        print(f"# decode4b {res['decode4b']}", file=sys.stderr, flush=True)
-    if want("shard"):
-        res["shard"] = guarded(lambda: bench_shard(ops, a.steps, a.warmup))
-        print(f"# shard {res['shard']}", file=sys.stderr, flush=True)
-    if want("norm"):
-        res["norm"] = guarded(lambda: bench_norm(ops, 2048, 32, 8, 32768, a.steps, a.warmup))
-        print(f"# norm {res['norm']}", file=sys.stderr, flush=True)
-    if "gemv" in only:
-        res["gemv"] = bench_gemv(a.steps, a.warmup)
-        print(f"# gemv {res['gemv']}", file=sys.stderr, flush=True)
-    if "qgemv" in only:
-        res["qgemv"] = bench_qgemv(a.steps, a.warmup)
-        print(f"# qgemv {res['qgemv']}", file=sys.stderr, flush=True)
-    if want("engine4b"):
-        def engine4b():
-            r = bench_engine()
-            # attention part of one decode step at the mean context of the run:
-            # 36 layers of the fused norm/RoPE/KV write + split-K + merge
-            r["attn_graph_ms"] = 36 * bench_fused_attention(
-                32, 8, int(r["mean_ctx"]), 1024, 36, a.steps, a.warmup)
-            return r
-        res["engine4b"] = guarded(engine4b)
-        print(f"# engine4b {res['engine4b']}", file=sys.stderr, flush=True)
-    if want("engine32b"):
-        res["engine32b"] = guarded(bench_engine32b)
-    if want("engine4b_q4km"):
-        res["engine4b_q4km"] = guarded(bench_engine_q)
-        print(f"# engine4b_q4km {res['engine4b_q4km']}", file=sys.stderr, flush=True)
-    if "engine4b_q5km" in only:
-        res["engine4b_q5km"] = guarded(lambda: bench_engine_q(base=13))
-        print(f"# engine4b_q5km {res['engine4b_q5km']}", file=sys.stderr, flush=True)
-
+def assemble_line(res, steps, warmup, cpu=None):
+    """The one JSON line from the measured sections in `res` (each as its
+    bench function returns it, or {"error": ...}) and the CPU baseline."""
     line = {"metric": "decode-attn HBM GB/s (% of peak) + prefill FMHA TFLOP/s (% MFMA peak)",
-            "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "higher_is_better": True,
+            "n_gpus": 1, "steps": steps, "warmup": warmup, "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic"}
     if "decode32b" in res:
         r = res["decode32b"]
@@ -1001,13 +925,6 @@ def main():
                         "512-token prompt, 256 greedy decode steps (decode-step hipGraph)",
             "decode_tok_s": round(r["tok_s"], 1), "decode_ms_per_token": round(r["decode_ms"], 4),
             "prefill_512_ms": round(r["prefill_ms"], 2),
-            "prefill_sweep": {str(pp): {"ms": round(ms, 2), "tok_s": round(pp / ms * 1e3, 1),
-                                        "reference_rtx5090_ms": REFERENCE_4B_RTX5090_PREFILL_MS[pp]}
-                              for pp, ms in r["prefill_sweep_ms"].items()},
-            "prefill_sweep_context": "whole-prompt prefill (embedding to last-token logits, "
-                                     "median of 3); reference_rtx5090_ms: grout's published "
-                                     "medians on one RTX 5090 (benchmarks/pytorch/README.md:"
-                                     "32-38; other hardware)",
             "weight_bytes": r["weight_bytes"],
             "weight_stream_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
     if ok("engine4b_q5km"):
@@ -1019,13 +936,6 @@ def main():
                         "512-token prompt, 256 greedy decode steps (decode-step hipGraph)",
             "decode_tok_s": round(r["tok_s"], 1), "decode_ms_per_token": round(r["decode_ms"], 4),
             "prefill_512_ms": round(r["prefill_ms"], 2),
-            "prefill_sweep": {str(pp): {"ms": round(ms, 2), "tok_s": round(pp / ms * 1e3, 1),
-                                        "reference_rtx5090_ms": REFERENCE_4B_RTX5090_PREFILL_MS[pp]}
-                              for pp, ms in r["prefill_sweep_ms"].items()},
-            "prefill_sweep_context": "whole-prompt prefill (embedding to last-token logits, "
-                                     "median of 3); reference_rtx5090_ms: grout's published "
-                                     "medians on one RTX 5090 (benchmarks/pytorch/README.md:"
-                                     "32-38; other hardware)",
             "weight_bytes": r["weight_bytes"],
             "weight_stream_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
     # sections that failed carry their error instead of numbers
@@ -1033,17 +943,98 @@ def main():
     for key, v in res.items():
         if isinstance(v, dict) and "error" in v:
             line[names.get(key, key)] = v
-    if not a.no_cpu and "decode32b" in res:
-        cb = guarded(cpu_baseline)
-
+    if cpu is not None:
         def rnd(v):
             if isinstance(v, float):
                 return round(v, 4)
             if isinstance(v, dict):
                 return {k: rnd(x) for k, x in v.items()}
             return v
-        line["cpu_baseline"] = rnd(cb)
-    print(json.dumps(line), flush=True)
+        line["cpu_baseline"] = rnd(cpu)
+    return line
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path "
+              f"(requested --gpus {a.gpus}); run with --gpus 1", file=sys.stderr)
+        return 2
+    import torch
+    import grout_amd
+    from grout_amd import ops
+
+    global GRAPH_TIMING
+    GRAPH_TIMING = not a.eager
+    grout_amd.lib()
+    if a.copy_calib:
+        src = torch.ones(128 << 20, dtype=torch.float16, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"# copy_calib: 3 copies of {src.numel() * 2} bytes", file=sys.stderr, flush=True)
+        del src, dst
+    only = set(filter(None, a.only.split(",")))
+    want = lambda k: not only or k in only
+    res = {}
+    if want("decode32b"):
+        res["decode32b_sweep"] = bench_decode32b_sweep(ops, (8192, 16384, 32768), a.steps,
+                                                       a.warmup)
+        res["decode32b"] = res["decode32b_sweep"][32768]
+        print(f"# decode32b {res['decode32b']}", file=sys.stderr, flush=True)
+    if want("prefill"):
+        sweep = guarded(lambda: {S: bench_prefill(ops, S, 32, 8,
+                                                  max(a.steps // (4 if S < 8192 else 10), 10),
+                                                  a.warmup)
+                                 for S in (512, 2048, 8192)})
+        if "error" in sweep:
+            res["prefill_error"] = sweep
+        else:
+            res["prefill_sweep"] = sweep
+            res["prefill"] = sweep[2048]
+        print(f"# prefill {sweep}", file=sys.stderr, flush=True)
+    if want("decode4b"):
+        def decode4b():
+            r = bench_decode(ops, 32, 8, 4096, 32768, 36, a.steps, a.warmup)
+            r["graph_ms"] = bench_decode_graph(grout_amd, 32, 8, 4096, 32768, 36,
+                                               max(a.steps // 4, 10), a.warmup)
+            return r
+        res["decode4b"] = guarded(decode4b)
+        print(f"# decode4b {res['decode4b']}", file=sys.stderr, flush=True)
+    if want("shard"):
+        res["shard"] = guarded(lambda: bench_shard(ops, a.steps, a.warmup))
+        print(f"# shard {res['shard']}", file=sys.stderr, flush=True)
+    if want("norm"):
+        res["norm"] = guarded(lambda: bench_norm(ops, 2048, 32, 8, 32768, a.steps, a.warmup))
+        print(f"# norm {res['norm']}", file=sys.stderr, flush=True)
+    if "gemv" in only:
+        res["gemv"] = bench_gemv(a.steps, a.warmup)
+        print(f"# gemv {res['gemv']}", file=sys.stderr, flush=True)
+    if "qgemv" in only:
+        res["qgemv"] = bench_qgemv(a.steps, a.warmup)
+        print(f"# qgemv {res['qgemv']}", file=sys.stderr, flush=True)
+    if want("engine4b"):
+        def engine4b():
+            r = bench_engine()
+            # attention part of one decode step at the mean context of the run:
+            # 36 layers of the fused norm/RoPE/KV write + split-K + merge
+            r["attn_graph_ms"] = 36 * bench_fused_attention(
+                32, 8, int(r["mean_ctx"]), 1024, 36, a.steps, a.warmup)
+            return r
+        res["engine4b"] = guarded(engine4b)
+        print(f"# engine4b {res['engine4b']}", file=sys.stderr, flush=True)
+    if want("engine32b"):
+        res["engine32b"] = guarded(bench_engine32b)
+    if want("engine4b_q4km"):
+        res["engine4b_q4km"] = guarded(bench_engine_q)
+        print(f"# engine4b_q4km {res['engine4b_q4km']}", file=sys.stderr, flush=True)
+    if "engine4b_q5km" in only:
+        res["engine4b_q5km"] = guarded(lambda: bench_engine_q(base=13))
+        print(f"# engine4b_q5km {res['engine4b_q5km']}", file=sys.stderr, flush=True)
+
+    cb = guarded(cpu_baseline) if not a.no_cpu and "decode32b" in res else None
+    print(json.dumps(assemble_line(res, a.steps, a.warmup, cb)), flush=True)
     return 0
 
 
