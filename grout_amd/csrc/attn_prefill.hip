@@ -43,12 +43,12 @@
 //    so each query row is one lane column and its softmax statistics live in
 //    the lanes that own its accumulator; row reductions across the four lane
 //    groups use v_permlane16/32_swap, row sums v_dot2 on the f16 P values;
-//  * speculative softmax: P is computed against the running max as it
-//    stands and checked through its own row sums; only a tile whose scores
-//    rise ~8 (log2 units) above the running max (and the first tile of a
-//    block) pays for the exact row max, the rescale and a second pass, so
-//    p stays <= 2^8 (exact in f16) and most tiles cost 2 VALU ops per score
-//    plus the exp2;
+//  * speculative softmax: P is computed against the reference point as it
+//    stands (the running max minus kPHeadroom) and checked through its own
+//    row sums; only a tile whose scores rise ~8 (log2 units) above the
+//    running max (and the first tile of a block) pays for the exact row max,
+//    the rescale and a second pass, so p stays below 2^15 (inside f16) and
+//    most tiles cost 2 VALU ops per score plus the exp2;
 //  * scheduling: block id -> (kv head = id mod Hkv, q block pair), so with
 //    Hkv = 8 each XCD's L2 holds one kv head's K/V.
 #include "common.hpp"
