@@ -130,8 +130,9 @@ def test_headers_compile_as_c11_and_a_c_caller_links(tmp_path):
 
 
 def test_integration_rust_block_declares_every_header_function():
-    """The Rust `extern "C"` block in INTEGRATION.md (what a maintainer would
-    paste into the FFI crate) declares exactly the functions the headers do."""
+    """The Rust `extern "C"` block of the integration notes (what a maintainer
+    would paste into the FFI crate) declares exactly the functions the headers
+    do."""
     text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     block = text[text.index("## 1."):text.index("## 2.")]
     declared = set(re.findall(r"pub fn (grout_[a-z0-9_]+)", block))
