@@ -117,6 +117,9 @@ def _decode_case(gpu, Hq, Hkv, ctx, max_ctx, num_splits, tag):
     (16, 1, 1500, 2048, None),    # one kv head (G = 16)
     (28, 4, 900, 1024, 5),        # Hkv = 4, G = 7
     (32, 16, 2000, 2048, None),   # Hkv = 16, G = 2
+    (12, 3, 2000, 2048, None),    # odd kv head counts: Hkv = 3, 5, 6
+    (80, 5, 777, 1024, 9),        # Hkv = 5, G = 16
+    (48, 6, 3001, 4096, None),    # Hkv = 6, G = 8, ragged
     (64, 8, 131072, 131072, 4096),  # GROUT_MAX_SPLITS: one 32-position tile per split, G = 8
     (16, 8, 3000, 4096, 4096),    # GROUT_MAX_SPLITS, 94 tiles: all but 94 splits empty
 ])
@@ -159,6 +162,7 @@ def test_decode_random_shapes_vs_oracle(gpu, Hq, Hkv, ctx, max_ctx, splits):
     (16, 1, 300, 512, None),      # one kv head
     (28, 4, 200, 256, 3),         # Hkv = 4, G = 7
     (32, 8, 4095, 4096, 4096),    # GROUT_MAX_SPLITS: the new row's split among 4000 empty ones
+    (24, 3, 300, 512, None),      # Hkv = 3, G = 8
 ])
 def test_fused_decode_step_vs_oracle(gpu, Hq, Hkv, pos, max_ctx, splits):
     """Norm/RoPE/KV write fused into the decode attention: cache rows
@@ -308,7 +312,8 @@ def test_decode_reuses_workspace_across_calls(gpu):
 @pytest.mark.parametrize("S,Hq,Hkv,pos0", [
     (1, 32, 8, 0), (17, 32, 8, 0), (64, 16, 8, 3), (200, 32, 8, 77), (130, 64, 8, 0),
     (96, 8, 8, 10), (77, 40, 8, 9), (33, 16, 1, 0), (150, 48, 8, 5), (111, 56, 8, 0),
-    (1, 32, 8, 4095), (3, 64, 8, 1000)])  # a one-token extend, a short chunk after a long prefix
+    (1, 32, 8, 4095), (3, 64, 8, 1000),  # a one-token extend, a short chunk after a long prefix
+    (100, 24, 3, 5), (70, 80, 5, 0), (300, 36, 6, 17)])  # Hkv = 3, 5, 6 (G = 8, 16, 6)
 def test_prefill_attention_vs_oracle(gpu, S, Hq, Hkv, pos0):
     _say("prefill", S, Hq, Hkv, pos0)
     max_ctx = pos0 + S + 5
