@@ -690,17 +690,20 @@ def test_engine_qwen3_32b_shapes_consistency(gpu):
         torch.cuda.empty_cache()
 
 
-@pytest.mark.parametrize("name,layers,hidden,inter,hq", [
-    ("8b", 36, 4096, 12288, 32),    # down K = 12288: 24 chunks, split over 4 waves
-    ("14b", 40, 5120, 17408, 40),   # down K = 17408: 34 chunks over 2 waves; G = 5
+@pytest.mark.parametrize("name,layers,hidden,inter,hq,tied", [
+    ("0.6b", 28, 1024, 3072, 16, True),     # q_dim 2048 = 2x hidden; tied head
+    ("1.7b", 28, 2048, 6144, 16, True),
+    ("8b", 36, 4096, 12288, 32, False),     # down K = 12288: 24 chunks, split over 4 waves
+    ("14b", 40, 5120, 17408, 40, False),    # down K = 17408: 34 chunks over 2 waves; G = 5
 ])
-def test_engine_qwen3_8b_14b_shapes_consistency(gpu, name, layers, hidden, inter, hq):
-    """Qwen3-8B / 14B shapes (8 kv heads, untied head, random N(0, 0.02) fp16
-    weights): decode at n equals a prefill of n + 1 (library GEMMs) through
-    the split-K long-K GEMVs and the norm-fused GEMVs at hidden 4096 / 5120."""
+def test_engine_qwen3_shapes_consistency(gpu, name, layers, hidden, inter, hq, tied):
+    """Qwen3-0.6B / 1.7B / 8B / 14B shapes (8 kv heads, random N(0, 0.02)
+    fp16 weights; the small two with the tied head they ship with): decode at
+    n equals a prefill of n + 1 (library GEMMs) through the GEMVs (split-K
+    long-K ones at 8B / 14B) and the norm-fused GEMVs at hidden 1024-5120."""
     from grout_amd.model import Engine, Qwen3Config, Qwen3Weights
 
-    cfg = Qwen3Config(layers, hidden, inter, hq, 8, 151936, tie_word_embeddings=False)
+    cfg = Qwen3Config(layers, hidden, inter, hq, 8, 151936, tie_word_embeddings=tied)
     w = Qwen3Weights.random(cfg, seed=1)
     eng = Engine(cfg, w, max_ctx=512)
     try:
