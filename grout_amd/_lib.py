@@ -133,6 +133,8 @@ SIGNATURES = {
     "grout_engine_warmup": (_i, [_p]),
     "grout_engine_position": (_i, [_p]),
     "grout_env_flag": (_i, [C.c_char_p, _i]),
+    "grout_env_usize": (C.c_long, [C.c_char_p, C.c_long]),
+    "grout_engine_num_splits": (_i, [_p]),
     "grout_engine_vram_preflight": (_i, [C.POINTER(Qwen3Config), _sz, _sz, _sz, _sz,
                                          C.POINTER(_sz)]),
     "grout_engine_uses_decode_graph": (_i, [_p]),

@@ -106,4 +106,24 @@ inline bool parse_bool_or(const char* raw, bool dflt) {
   return dflt;
 }
 
+// A positive integer setting as the reference's env_usize_or reads one
+// (src/model.rs:204-210, Rust's usize parsing): an optional '+' and decimal
+// digits, nothing else (no whitespace); zero, a value past 2^63 - 1 (the
+// result is a long), anything else or an unset variable (raw == NULL) give
+// the default.
+inline long parse_usize_or(const char* raw, long dflt) {
+  if (raw == nullptr) return dflt;
+  const char* c = raw;
+  if (*c == '+') ++c;
+  if (*c == '\0') return dflt;
+  unsigned long long v = 0;
+  for (; *c; ++c) {
+    if (*c < '0' || *c > '9') return dflt;
+    if (v > (~0ULL - 9) / 10) return dflt;  // past 64 bits: Rust's parse fails
+    v = v * 10 + (unsigned long long)(*c - '0');
+  }
+  if (v == 0) return dflt;
+  return v > (unsigned long long)0x7fffffffffffffffLL ? dflt : (long)v;
+}
+
 }  // namespace grout_abi

@@ -636,7 +636,14 @@ int create_impl(grout_engine* e, const grout_qwen3_config* c, const void* final_
   e->kv_dim = c->num_kv_heads * 128;
   e->qkv_dim = e->q_dim + 2 * e->kv_dim;
   e->head_stride = (long)c->max_ctx * 128;
-  e->num_splits = grout_attn_decode_default_splits(c->max_ctx, c->num_q_heads, c->num_kv_heads);
+  // GROUT_FMHA_NUM_KV_SPLITS overrides the decode split count, as the
+  // reference's does (src/model.rs:2713-2714), capped at GROUT_MAX_SPLITS.
+  {
+    const long dflt =
+        grout_attn_decode_default_splits(c->max_ctx, c->num_q_heads, c->num_kv_heads);
+    const long ns = parse_usize_or(std::getenv("GROUT_FMHA_NUM_KV_SPLITS"), dflt);
+    e->num_splits = (int)(ns < GROUT_MAX_SPLITS ? ns : GROUT_MAX_SPLITS);
+  }
   e->ws_bytes = decode_ws_bytes(c->num_q_heads, c->num_kv_heads, e->num_splits);
   e->argmax_blocks = grout::argmax_num_blocks(c->vocab_size);
   e->qk_scale = 1.0f / std::sqrt(128.0f);  // src/model.rs:2654, 6901
@@ -1150,6 +1157,12 @@ int grout_engine_position(const grout_engine* e) { return e ? e->next_pos : -1; 
 int grout_env_flag(const char* value, int default_value) {
   return parse_bool_or(value, default_value != 0) ? 1 : 0;
 }
+
+long grout_env_usize(const char* value, long default_value) {
+  return parse_usize_or(value, default_value);
+}
+
+int grout_engine_num_splits(const grout_engine* e) { return e ? e->num_splits : -1; }
 
 int grout_engine_vram_preflight(const grout_qwen3_config* c, size_t weight_bytes,
                                 size_t scratch_bytes, size_t free_bytes, size_t total_bytes,

@@ -481,6 +481,12 @@ class Engine:
         return int(lib().grout_engine_position(self._h))
 
     @property
+    def num_splits(self) -> int:
+        """Decode attention split count (GROUT_FMHA_NUM_KV_SPLITS, else the
+        library's default for max_ctx)."""
+        return int(lib().grout_engine_num_splits(self._h))
+
+    @property
     def uses_decode_graph(self) -> bool:
         """True when decode replays the captured decode-step graph."""
         return bool(lib().grout_engine_uses_decode_graph(self._h))

@@ -390,6 +390,13 @@ int grout_engine_warmup(grout_engine* engine);
 /* Position the next decode writes (number of tokens in the session). */
 int grout_engine_position(const grout_engine* engine);
 
+/* Split count of the engine's decode attention: GROUT_FMHA_NUM_KV_SPLITS
+ * from the environment at creation (read as grout_env_usize does, capped at
+ * GROUT_MAX_SPLITS; the reference's knob of the same name,
+ * src/model.rs:2713-2714), else grout_attn_decode_default_splits(max_ctx).
+ * -1 for NULL. */
+int grout_engine_num_splits(const grout_engine* engine);
+
 /* Host only.  How the engine reads a boolean switch from the environment
  * (GROUT_HIP_GRAPH_DECODE, the counterpart of the reference's
  * GROUT_CUDA_GRAPH_DECODE): `value` is the variable's text, NULL when unset.
@@ -397,6 +404,13 @@ int grout_engine_position(const grout_engine* engine);
  * or "" (whitespace trimmed, case ignored), default_value (0 or 1) for
  * anything else or NULL.  Mirrors env_bool_or (src/model.rs:212-224). */
 int grout_env_flag(const char* value, int default_value);
+
+/* Host only.  How the engine reads a positive integer setting
+ * (GROUT_FMHA_NUM_KV_SPLITS): an optional '+' and decimal digits, nothing
+ * else; zero, a value past 2^63 - 1 (a long; Rust's usize takes up to
+ * 2^64 - 1), any other text or NULL give default_value.  Mirrors
+ * env_usize_or (src/model.rs:204-210). */
+long grout_env_usize(const char* value, long default_value);
 
 /* Frees everything the engine owns (not the weights).  NULL is a no-op. */
 int grout_engine_destroy(grout_engine* engine);

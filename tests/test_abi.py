@@ -377,6 +377,20 @@ def test_env_flag_parses_like_env_bool_or():
     assert L.grout_env_flag(None, 1) == 1 and L.grout_env_flag(None, 0) == 0
 
 
+def test_env_usize_parses_like_env_usize_or():
+    """GROUT_FMHA_NUM_KV_SPLITS is read like the reference's env_usize_or
+    (src/model.rs:204-210, Rust's usize parse): an optional '+' and decimal
+    digits; zero, whitespace, signs other than '+', other text, overflow or
+    unset give the default."""
+    L = grout_amd.lib()
+    for raw, want in ((b"16", 16), (b"+7", 7), (b"007", 7), (b"4096", 4096),
+                      (b"18446744073709551615", 17), (b"18446744073709551616", 17),
+                      (b"0", 17), (b"-3", 17), (b" 16", 17), (b"16 ", 17), (b"", 17),
+                      (b"+", 17), (b"1e3", 17), (b"0x10", 17), (b"abc", 17), (None, 17)):
+        assert L.grout_env_usize(raw, 17) == want, raw
+    assert L.grout_env_usize(b"9223372036854775807", 5) == 9223372036854775807
+
+
 def test_low_bit_k_limit_covers_qwen3_without_gpu():
     """The low-bit GEMVs stage x in LDS: every Qwen3 ffn_down width up to
     32B's 25600 is accepted, K past 32768 is refused (host-side sizing)."""

@@ -354,6 +354,37 @@ def test_engine_chunked_prefill_vs_oracle(gpu, name, chunks):
         eng.close()
 
 
+def test_engine_split_count_from_the_environment(gpu, monkeypatch):
+    """GROUT_FMHA_NUM_KV_SPLITS sets the decode split count when an engine is
+    created (the reference's knob, src/model.rs:2713-2714): the engine
+    reports it, "0" keeps the default, values past GROUT_MAX_SPLITS are
+    capped, and the decode logits agree with a default engine's."""
+    cfg = tiny_configs()["4b-dims-2l"]
+    host_w = Q.random_host_weights(cfg, seed=3, std=0.02)
+    prompt = np.random.default_rng(80).integers(0, cfg.vocab_size, 80)
+    engines = {}
+    for raw in (None, "3", "0", "99999"):
+        if raw is None:
+            monkeypatch.delenv("GROUT_FMHA_NUM_KV_SPLITS", raising=False)
+        else:
+            monkeypatch.setenv("GROUT_FMHA_NUM_KV_SPLITS", raw)
+        engines[raw] = make_engine(cfg, host_w, 1024)
+    try:
+        default = engines[None].num_splits
+        assert default == 32
+        assert [engines[r].num_splits for r in ("3", "0", "99999")] == [3, default, 4096]
+        outs = {}
+        for raw, eng in engines.items():
+            eng.prefill(prompt)
+            outs[raw] = [eng.decode(t).values for t in (5, 77)]
+        for raw in ("3", "99999"):
+            for i in range(2):
+                check_logits(outs[raw][i], outs[None][i], f"splits {raw} vs default, step {i}")
+    finally:
+        for eng in engines.values():
+            eng.close()
+
+
 def test_engine_extend_errors(gpu):
     from grout_amd._lib import GroutError
 
