@@ -363,7 +363,7 @@ def test_engine_split_count_from_the_environment(gpu, monkeypatch):
     host_w = Q.random_host_weights(cfg, seed=3, std=0.02)
     prompt = np.random.default_rng(80).integers(0, cfg.vocab_size, 80)
     engines = {}
-    for raw in (None, "3", "0", "99999"):
+    for raw in (None, "3", "1", "0", "99999"):
         if raw is None:
             monkeypatch.delenv("GROUT_FMHA_NUM_KV_SPLITS", raising=False)
         else:
@@ -372,12 +372,12 @@ def test_engine_split_count_from_the_environment(gpu, monkeypatch):
     try:
         default = engines[None].num_splits
         assert default == 32
-        assert [engines[r].num_splits for r in ("3", "0", "99999")] == [3, default, 4096]
+        assert [engines[r].num_splits for r in ("3", "1", "0", "99999")] == [3, 1, default, 4096]
         outs = {}
         for raw, eng in engines.items():
             eng.prefill(prompt)
             outs[raw] = [eng.decode(t).values for t in (5, 77)]
-        for raw in ("3", "99999"):
+        for raw in ("3", "1", "99999"):  # "1": one pass, no merge launch
             for i in range(2):
                 check_logits(outs[raw][i], outs[None][i], f"splits {raw} vs default, step {i}")
     finally:
