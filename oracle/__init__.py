@@ -22,7 +22,9 @@ Parity pinning (what checks each function independently of its own formula):
 * ``attention_prefill_rows`` / ``attention_decode``: torch float64
   ``scaled_dot_product_attention`` with GQA (a library implementation),
   brute-force float64 softmax on tiny shapes, closed forms (V constant,
-  K constant, ctx=1, q = lambda*k_j), GQA == MHA with repeated K/V.
+  K constant, ctx=1, q = lambda*k_j), GQA == MHA with repeated K/V; the
+  benchmark configurations against committed torch float64 fixtures
+  (tests/golden/).
 * ``decode_split`` + ``splitk_merge``: equal to ``attention_decode`` for every
   split count, including empty splits.
 """
