@@ -91,8 +91,9 @@ template <int WAVES, bool FUSED, bool DIRECT>
 __global__ __launch_bounds__(WAVES * 64, (WAVES <= 4 ? 2 : 1)) void attn_decode_split_kernel(
     const half_t* __restrict__ q, const half_t* __restrict__ k_cache,
     const half_t* __restrict__ v_cache, long head_stride, const uint32_t* __restrict__ d_pos,
-    int max_ctx, int G, int nsplit, float scale_log2, float* __restrict__ part_acc,
-    float* __restrict__ part_ml, DecodeFused fz, half_t* __restrict__ out) {
+    int max_ctx, int G, int nsplit, uint32_t split_magic, float scale_log2,
+    float* __restrict__ part_acc, float* __restrict__ part_ml, DecodeFused fz,
+    half_t* __restrict__ out) {
   // Wave w's tile buffer is s_buf[w].
   __shared__ __attribute__((aligned(1024))) unsigned char s_buf[WAVES][kSlotBytes];
   __shared__ float s_ml[WAVES][16][2];
@@ -106,20 +107,43 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES <= 4 ? 2 : 1)) void attn_decode_
   // FUSED: rotated q rows of the group, then the new K and V rows.
   __shared__ __attribute__((aligned(16))) half_t s_qkv[FUSED ? 18 : 1][kHeadDim];
 
-  // block id = split * Hkv + kvh: workgroups are dealt to the 8 XCDs round
-  // robin, so with Hkv = 8 every split of a kv head runs on one XCD and its
-  // partials stay in that XCD's L2 for the merge (which uses the same map)
-  const int Hkv = (int)gridDim.x / nsplit;
-  const int kvh = (int)blockIdx.x % Hkv, split = (int)blockIdx.x / Hkv;
+  // Grid (Hkv, nsplit): workgroup (kvh, split) has the linear id
+  // split * Hkv + kvh, and workgroups are dealt to the 8 XCDs round robin in
+  // that order, so with Hkv = 8 every split of a kv head runs on one XCD and
+  // its partials stay in that XCD's L2 for the merge (which uses the same
+  // map).  Two grid dimensions instead of one id spare the divisions that
+  // would split it.
+  const int Hkv = (int)gridDim.x;
+  const int kvh = (int)blockIdx.x, split = (int)blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15, kb = lane >> 4;
   const int wave_off = w * kSlotBytes;  // folded into the per-lane offsets below
 
+  // Everything up to the first tile's loads waits for the position, so the
+  // chain after it has no integer division (a runtime one is ~20 dependent
+  // instructions), and the q rows (independent of it) are requested first.
   const uint32_t pos = d_pos[0];
+  half8 qf[4];
+  if constexpr (!FUSED) {
+    // Columns past the group hold a copy of head G-1 (same cache lines, no
+    // branch in front of the tile loads, and no select that would wait for
+    // these loads before the loop).  Every column's softmax is its own and
+    // a copy rescales exactly when head G-1 does, so the wave-wide rescale
+    // decision and the group's outputs are those of the G heads; the copies'
+    // columns are never written.
+    const int qc = col < G ? col : G - 1;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      qf[c] = as_half8(load16(q + ((size_t)kvh * G + qc) * kHeadDim + c * 32 + kb * 8));
+  }
   const int s_kv = pos >= (uint32_t)max_ctx ? max_ctx : (int)pos + 1;  // always in [1, max_ctx]
   const int ntiles = (s_kv + kTile - 1) / kTile;
-  const int per = (ntiles + nsplit - 1) / nsplit;
+  // per = ceil(ntiles / nsplit): split_magic = ceil(2^31 / nsplit) = (2^31 + e)
+  // / nsplit with 0 <= e < nsplit, so x * split_magic / 2^31 = x / nsplit +
+  // x e / (nsplit 2^31), whose floor is floor(x / nsplit) while x e < 2^31:
+  // here x < 2^18 + 2^12 (ntiles <= GROUT_MAX_CTX / 16, nsplit <= 4096).
+  const int per = (int)__umulhi(2u * (uint32_t)(ntiles + nsplit - 1), split_magic);
   const int t0 = split * per;
   const int t1 = min(t0 + per, ntiles);
   // this wave's tiles: t0 + w + WAVES k, k = 0 .. nmine-1
@@ -129,10 +153,20 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES <= 4 ? 2 : 1)) void attn_decode_
   // (cyclically; rot is a multiple of WAVES, so the tile sets stay disjoint).
   // Splits start 256 KiB apart at 32k; staggering where each one starts
   // spreads the concurrent reads over more HBM channels (measured a few
-  // percent at 4k context, within noise at 32k).
+  // percent at 4k context, within noise at 32k).  rot = (x mod P) * WAVES,
+  // P = len / WAVES, x = split * 7 + kvh * 3 (kept below 2^22): the quotient
+  // through the hardware reciprocal is off by at most one for these
+  // magnitudes, and one correction makes the remainder exact.
   const int len = t1 - t0;
-  const int rot =
-      len > 0 && len % WAVES == 0 ? ((split * 7 + kvh * 3) % (len / WAVES)) * WAVES : 0;
+  int rot = 0;
+  {
+    const int P = len / WAVES;
+    const int x = (split * 7 + kvh * 3) & 0x3fffff;
+    const int qe = (int)((float)x * __builtin_amdgcn_rcpf((float)max(P, 1)));
+    int rm = x - qe * P;
+    rm = rm < 0 ? rm + P : (rm >= P ? rm - P : rm);
+    rot = len > 0 && len % WAVES == 0 ? rm * WAVES : 0;
+  }
   auto tile_of = [&](int k) __attribute__((always_inline)) {
     const int x = w + WAVES * k + rot;
     return t0 + (x >= len ? x - len : x);
@@ -228,17 +262,11 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES <= 4 ? 2 : 1)) void attn_decode_
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   }
 
-  half8 qf[4];
+  if constexpr (FUSED) {
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    if (col < G) {
-      if constexpr (FUSED)
-        qf[c] = as_half8(*reinterpret_cast<const u32x4*>(&s_qkv[col][c * 32 + kb * 8]));
-      else
-        qf[c] = as_half8(load16(q + ((size_t)kvh * G + col) * kHeadDim + c * 32 + kb * 8));
-    } else {
-      qf[c] = as_half8(u32x4{0u, 0u, 0u, 0u});
-    }
+    for (int c = 0; c < 4; ++c)
+      qf[c] = col < G ? as_half8(*reinterpret_cast<const u32x4*>(&s_qkv[col][c * 32 + kb * 8]))
+                      : as_half8(u32x4{0u, 0u, 0u, 0u});
   }
 
   int st_off[4];
@@ -411,7 +439,8 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES <= 4 ? 2 : 1)) void attn_decode_
 }
 
 // Merge: one 128-thread workgroup per (query head h = kvh*G + g, half of D),
-// block id = (2g + half) * Hkv + kvh (the split pass's XCD map).  The split
+// grid (Hkv, 2G), linear id (2g + half) * Hkv + kvh (the split pass's XCD
+// map).  The split
 // weights 2^(m_s - M) use the hardware exp2 (v_exp_f32): it differs from the
 // library exp2f only below 2^-126, i.e. for splits whose max trails the
 // overall max by more than 126 (log2 units), whose weight is nil either way;
@@ -427,12 +456,12 @@ __global__ __launch_bounds__(128) void attn_decode_merge_kernel(
     half_t* __restrict__ out, int G, int nsplit, uint32_t* __restrict__ advance_pos) {
   // The split pass that precedes this launch has read the position: this
   // kernel never does, so it may move the word on to the next step's.
-  if (advance_pos != nullptr && blockIdx.x == 0 && threadIdx.x == 0) advance_pos[0] += 1u;
+  if (advance_pos != nullptr && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0)
+    advance_pos[0] += 1u;
   __shared__ float s_m[kMergeGroups][16];
   __shared__ float s_l[kMergeGroups][16];
   __shared__ floatx4 s_o[kMergeGroups][16];
-  const int Hkv = (int)gridDim.x / (2 * G);
-  const int kvh = (int)blockIdx.x % Hkv, rest = (int)blockIdx.x / Hkv;
+  const int kvh = (int)blockIdx.x, rest = (int)blockIdx.y;
   const int half = rest & 1, g = rest >> 1, h = kvh * G + g;
   const int dq = threadIdx.x & 15, sg = threadIdx.x >> 4;
   const int d0 = half * 64 + dq * 4;
@@ -474,15 +503,22 @@ __global__ __launch_bounds__(128) void attn_decode_merge_kernel(
   }
 }
 
+// ceil(2^31 / nsplit), the multiplier of the split kernel's division-free
+// ceil(ntiles / nsplit) (nsplit in [1, GROUT_MAX_SPLITS]).
+static uint32_t split_magic(int nsplit) {
+  return (uint32_t)(((1ull << 31) + (unsigned long long)nsplit - 1) / (unsigned long long)nsplit);
+}
+
 hipError_t launch_attn_decode_split(const void* q, const void* k_cache, const void* v_cache,
                                     long head_stride, const uint32_t* d_pos, int max_ctx,
                                     int Hq, int Hkv, int nsplit, float qk_scale,
                                     float* part_acc, float* part_ml, hipStream_t stream) {
   const float scale_log2 = qk_scale * 1.4426950408889634f;
-  const unsigned grid = (unsigned)(nsplit * Hkv);
-  attn_decode_split_kernel<kDecWaves, false, false><<<grid, kDecWaves * 64, 0, stream>>>(
-      (const half_t*)q, (const half_t*)k_cache, (const half_t*)v_cache, head_stride, d_pos,
-      max_ctx, Hq / Hkv, nsplit, scale_log2, part_acc, part_ml, DecodeFused{}, nullptr);
+  attn_decode_split_kernel<kDecWaves, false, false>
+      <<<dim3((unsigned)Hkv, (unsigned)nsplit), kDecWaves * 64, 0, stream>>>(
+          (const half_t*)q, (const half_t*)k_cache, (const half_t*)v_cache, head_stride, d_pos,
+          max_ctx, Hq / Hkv, nsplit, split_magic(nsplit), scale_log2, part_acc, part_ml,
+          DecodeFused{}, nullptr);
   return hipGetLastError();
 }
 
@@ -498,15 +534,15 @@ hipError_t launch_attn_decode_fused(const void* qkv, const void* gamma_q, const 
   if (Hq / Hkv > 16) return hipErrorInvalidValue;
   if (nsplit == 1) {
     attn_decode_split_kernel<kDirectWaves, true, true>
-        <<<(unsigned)Hkv, kDirectWaves * 64, 0, stream>>>(
+        <<<dim3((unsigned)Hkv, 1u), kDirectWaves * 64, 0, stream>>>(
             nullptr, (const half_t*)k_cache, (const half_t*)v_cache, head_stride, d_pos, max_ctx,
-            Hq / Hkv, 1, scale_log2, nullptr, nullptr, fz, (half_t*)out);
+            Hq / Hkv, 1, split_magic(1), scale_log2, nullptr, nullptr, fz, (half_t*)out);
     return hipGetLastError();
   }
   attn_decode_split_kernel<kDecWaves, true, false>
-      <<<(unsigned)(nsplit * Hkv), kDecWaves * 64, 0, stream>>>(
+      <<<dim3((unsigned)Hkv, (unsigned)nsplit), kDecWaves * 64, 0, stream>>>(
           nullptr, (const half_t*)k_cache, (const half_t*)v_cache, head_stride, d_pos, max_ctx,
-          Hq / Hkv, nsplit, scale_log2, part_acc, part_ml, fz, nullptr);
+          Hq / Hkv, nsplit, split_magic(nsplit), scale_log2, part_acc, part_ml, fz, nullptr);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   return launch_attn_decode_merge(part_acc, part_ml, out, Hq, Hkv, nsplit, stream, advance_pos);
@@ -515,7 +551,7 @@ hipError_t launch_attn_decode_fused(const void* qkv, const void* gamma_q, const 
 hipError_t launch_attn_decode_merge(const float* part_acc, const float* part_ml, void* out,
                                     int Hq, int Hkv, int nsplit, hipStream_t stream,
                                     uint32_t* advance_pos) {
-  attn_decode_merge_kernel<<<(unsigned)(2 * Hq), 128, 0, stream>>>(
+  attn_decode_merge_kernel<<<dim3((unsigned)Hkv, (unsigned)(2 * (Hq / Hkv))), 128, 0, stream>>>(
       part_acc, part_ml, (half_t*)out, Hq / Hkv, nsplit, advance_pos);
   return hipGetLastError();
 }
