@@ -359,10 +359,18 @@ struct SRaw {
   uint32_t d;
 };
 
+// u / UPR without an integer division (one in front of the staging loads
+// would delay every load issued after them): for u < R * UPR <= 2^15,
+// (u + 1/2) / UPR lies at least 1/(2 UPR) >= 2^-11 from an integer, and the
+// product with the hardware reciprocal (1 ulp) is within 2^-17 of it.
+__device__ __forceinline__ int unit_row(int u, float inv_upr) {
+  return (int)(((float)u + 0.5f) * inv_upr);
+}
+
 template <int FMT, bool SILU, int R>
 __device__ __forceinline__ SRaw stage_load(const uint8_t* __restrict__ W, const QLayout& L, int u,
-                                           int UPR, int N, int K) {
-  const int lr = u / UPR, k = u - lr * UPR;
+                                           int UPR, float inv_upr, int N, int K) {
+  const int lr = unit_row(u, inv_upr), k = u - lr * UPR;
   int o;
   const int row = qrow<SILU, R>(lr, N, o);
   SRaw s;
@@ -384,10 +392,10 @@ __device__ __forceinline__ SRaw stage_load(const uint8_t* __restrict__ W, const 
 // native layout, d * sc and dmin * m in fp32), times the power of two that
 // undoes the denormal encoding (exact).
 template <int FMT>
-__device__ __forceinline__ void stage_store(const SRaw& s, int u, int U, int UPR, int SCW,
-                                            float* s_sc) {
+__device__ __forceinline__ void stage_store(const SRaw& s, int u, int U, int UPR, float inv_upr,
+                                            int SCW, float* s_sc) {
   if (u >= U) return;
-  const int lr = u / UPR, k = u - lr * UPR;
+  const int lr = unit_row(u, inv_upr), k = u - lr * UPR;
   float* dst = s_sc + lr * SCW;
   if (FMT == 8) {
     dst[k] = h2f_bits((uint16_t)s.d) * 0x1p24f;
@@ -547,6 +555,7 @@ __global__ __launch_bounds__(R * S * kQTeam) void gemv_q_kernel(const uint8_t* _
   float* const s_sc = s_xsum + (FMT == 8 ? K / 32 : K / 16);
   const int SCW = FMT == 8 ? K / 32 : K / 16;
   const int UPR = FMT == 8 ? K / 32 : K / 256;  // staging units per row
+  const float inv_upr = __builtin_amdgcn_rcpf((float)UPR);
   const int U = R * UPR, NG = K / 8, P = K / 32;
   const int tid = threadIdx.x, slice = tid / (R * kQTeam), team = (tid >> 4) % R, m = tid & 15;
   int out;
@@ -577,7 +586,7 @@ __global__ __launch_bounds__(R * S * kQTeam) void gemv_q_kernel(const uint8_t* _
     SRaw ur[NUJ];
 #pragma unroll
     for (int j = 0; j < NUJ; ++j)
-      ur[j] = stage_load<FMT, SILU, R>(W, L, min(tid + T * j, U - 1), UPR, N, K);
+      ur[j] = stage_load<FMT, SILU, R>(W, L, min(tid + T * j, U - 1), UPR, inv_upr, N, K);
     QPc raw[B];
 #pragma unroll
     for (int b = 0; b < B; ++b) raw[b] = qpc_load<FMT>(W, L, row, m + 16 * (st + b), K);
@@ -597,7 +606,7 @@ __global__ __launch_bounds__(R * S * kQTeam) void gemv_q_kernel(const uint8_t* _
 #pragma unroll
     for (int j = 0; j < NXJ; ++j) stage_x<FMT>(xr[j], tid + T * j, NG, s_x, s_xsum);
 #pragma unroll
-    for (int j = 0; j < NUJ; ++j) stage_store<FMT>(ur[j], tid + T * j, U, UPR, SCW, s_sc);
+    for (int j = 0; j < NUJ; ++j) stage_store<FMT>(ur[j], tid + T * j, U, UPR, inv_upr, SCW, s_sc);
     __syncthreads();
     const int fs = FMT == 8 ? 16 : 32;  // scale / x-sum floats per piece step
     qconsume<FMT, NPW, B, 0>(raw, acc, st, i0, m, q,
@@ -625,7 +634,8 @@ __global__ __launch_bounds__(R * S * kQTeam) void gemv_q_kernel(const uint8_t* _
       stage_x<FMT>(xv, c, NG, s_x, s_xsum);
     }
     for (int u = tid; u < U; u += T)
-      stage_store<FMT>(stage_load<FMT, SILU, R>(W, L, u, UPR, N, K), u, U, UPR, SCW, s_sc);
+      stage_store<FMT>(stage_load<FMT, SILU, R>(W, L, u, UPR, inv_upr, N, K), u, U, UPR, inv_upr,
+                       SCW, s_sc);
     __syncthreads();
     const int npl = (P + 15) / 16;
     const int fs = FMT == 8 ? 16 : 32;
