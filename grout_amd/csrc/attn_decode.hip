@@ -454,10 +454,6 @@ constexpr int kMergeGroups = 8;
 __global__ __launch_bounds__(128) void attn_decode_merge_kernel(
     const float* __restrict__ part_acc, const float* __restrict__ part_ml,
     half_t* __restrict__ out, int G, int nsplit, uint32_t* __restrict__ advance_pos) {
-  // The split pass that precedes this launch has read the position: this
-  // kernel never does, so it may move the word on to the next step's.
-  if (advance_pos != nullptr && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0)
-    advance_pos[0] += 1u;
   __shared__ float s_m[kMergeGroups][16];
   __shared__ float s_l[kMergeGroups][16];
   __shared__ floatx4 s_o[kMergeGroups][16];
@@ -501,6 +497,11 @@ __global__ __launch_bounds__(128) void attn_decode_merge_kernel(
     for (int i = 0; i < 4; ++i) o[i] = (half_t)(Ot[i] * inv);
     *reinterpret_cast<u32x2*>(out + (size_t)h * kHeadDim + d0) = __builtin_bit_cast(u32x2, o);
   }
+  // The split pass that precedes this launch has read the position: this
+  // kernel never does, so it may move the word on to the next step's (last,
+  // so that the partials' loads go out first).
+  if (advance_pos != nullptr && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0)
+    advance_pos[0] += 1u;
 }
 
 // ceil(2^31 / nsplit), the multiplier of the split kernel's division-free
