@@ -103,6 +103,9 @@ __device__ __forceinline__ void lds_barrier() {
 // are complete.
 __device__ __forceinline__ void wait_vm_keep8() { asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); }
 __device__ __forceinline__ void wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// s_waitcnt immediate for vmcnt(0) alone (gfx9 fields: vmcnt bits 3:0 and
+// 15:14 = 0, expcnt bits 6:4 = 7, lgkmcnt bits 11:8 = 15, i.e. no wait).
+constexpr int kVmcnt0 = 0x0F70;
 
 // Lane l ends with f(x[l], x[l ^ 16]) and then f(.., x[l ^ 32]): the reduction
 // over the four 16-lane groups that hold one MFMA column.
@@ -510,21 +513,33 @@ __global__ __launch_bounds__(512, 1) void fmha_prefill_kernel(
   // Team B loads its Q only after the first barrier (it idles one phase
   // anyway), so team A's Q is not slowed by the other half of the burst of Q
   // reads that opens the kernel on every CU at once.
+  // K(0) and team A's Q go out first and are all that the first barrier
+  // waits for: V(0) and K(1) (the 8 most recent loads of each wave) land
+  // under S(0) = K(0).Q^T and team A's first softmax.  The closing wait of
+  // each team's first S phase (vmcnt(8): everything but that phase's own 8
+  // loads) covers them before the barrier ahead of their first reader, the
+  // G phase of tile 0.
   if (n > 0) {
     dma_tile(is_k, kh, tile_at(0), k0);
+    if (team == 0) load_q(qb0);
+    __builtin_amdgcn_sched_barrier(0);
     dma_tile(is_v, vh, tile_at(0), v0);
     dma_tile(is_k, kh, tile_at(min(1, n - 1)), k1);
-    if (team == 0) load_q(qb0);
   }
-  wait_vm_all();
+  wait_vm_keep8();
   lds_barrier();
   // Phase count after this point: A runs 1 + 2*nA phases, B one idle phase
   // plus 1 + 2*nB; the shorter team pads with empty phases.
   const int total = max(1 + 2 * a, 2 + 2 * nB);
   int mine = 0;
   if (team == 1) {
-    if (n > 0) load_q(qb0);  // waited for before its first S.K^T (vmcnt)
+    if (n > 0) load_q(qb0);
     lds_barrier();
+    // Its Q (and V(0), K(1) before it) complete, in a wait the compiler
+    // sees: on the code both teams share from here, team A's path then
+    // needs only vmcnt(8) (its V(0) and K(1) stay in flight), where a wait
+    // for team B's Q, the most recent loads, would be vmcnt(0) for both.
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
     mine = 1;
   }
   if (n > 0) qk_only(k0);
