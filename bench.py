@@ -41,6 +41,9 @@ def parse():
     ap.add_argument("--eager", action="store_true",
                     help="launch the timed calls from the host instead of replaying a captured "
                          "graph (for per-dispatch counter collection)")
+    ap.add_argument("--decode-splits", type=int, default=None,
+                    help="Qwen3-32B decode: this split count at every context instead of the "
+                         "per-context sweep (1-4096)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run a plain 256 MiB device copy (HBM counter calibration)")
     return ap.parse_args()
@@ -215,17 +218,20 @@ def bench_decode(ops, Hq, Hkv, ctx, max_ctx, n_layers, steps, warmup, num_splits
 DECODE32B_SPLITS = (8, 16, 24, 32, 40, 48, 64)
 
 
-def bench_decode32b_sweep(ops, ctxs, steps, warmup, sweep_steps=100):
+def bench_decode32b_sweep(ops, ctxs, steps, warmup, sweep_steps=100, splits=None):
     """Config 4: Qwen3-32B decode attention (Hq=64, Hkv=8) at each context.
     The split count is swept first (sweep_steps graph-replayed steps of split
     pass + merge per candidate), as the reference tunes FMHA_NUM_KV_SPLITS per
     context (src/model.rs:135-141, benchmarks/sweep_tg_sm100.sh:32-43); the
     fastest is then timed afresh over `steps` steps, so the reported time is
-    not the minimum of the sweep's samples."""
+    not the minimum of the sweep's samples.  splits: one count to use at every
+    context instead of the sweep (e.g. under a profiler, whose per-dispatch
+    overhead moves the sweep's pick)."""
     b = DecodeBench(64, 8, 32768, 4)
     out = {}
     for ctx in ctxs:
-        sweep = {ns: b.time_step(ctx, ns, sweep_steps, warmup) for ns in DECODE32B_SPLITS}
+        sweep = {ns: b.time_step(ctx, ns, sweep_steps, warmup)
+                 for ns in ((splits,) if splits else DECODE32B_SPLITS)}
         best = min(sweep, key=sweep.get)
         step_ms, step_dist = b.time_step(ctx, best, steps, warmup, dist=True)
         split_ms, split_dist = b.time_split(ctx, best, steps, warmup, dist=True)
@@ -960,6 +966,10 @@ def main():
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
               f"(requested --gpus {a.gpus}); run with --gpus 1", file=sys.stderr)
         return 2
+    if a.decode_splits is not None and not 1 <= a.decode_splits <= 4096:
+        print(f"--decode-splits {a.decode_splits}: the split count must be in [1, 4096]",
+              file=sys.stderr)
+        return 2
     import torch
     import grout_amd
     from grout_amd import ops
@@ -980,7 +990,7 @@ def main():
     res = {}
     if want("decode32b"):
         res["decode32b_sweep"] = bench_decode32b_sweep(ops, (8192, 16384, 32768), a.steps,
-                                                       a.warmup)
+                                                       a.warmup, splits=a.decode_splits)
         res["decode32b"] = res["decode32b_sweep"][32768]
         print(f"# decode32b {res['decode32b']}", file=sys.stderr, flush=True)
     if want("prefill"):

@@ -15,6 +15,17 @@ def test_bench_refuses_more_than_one_gpu():
     assert r.stdout == ""
 
 
+def test_bench_refuses_a_split_count_outside_the_abi_range():
+    # --decode-splits pins the Qwen3-32B split count; outside [1, 4096] it exits
+    # with status 2 before touching a GPU
+    for bad in ("0", "4097"):
+        r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--decode-splits", bad],
+                           cwd=ROOT, capture_output=True, text=True, timeout=120)
+        assert r.returncode == 2, r.stderr
+        assert "[1, 4096]" in r.stderr
+        assert r.stdout == ""
+
+
 def test_guarded_section_records_its_error():
     # a secondary section that raises leaves an error entry, not a missing line
     sys.path.insert(0, ROOT)
