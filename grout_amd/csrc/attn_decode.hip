@@ -440,10 +440,9 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES <= 4 ? 2 : 1)) void attn_decode_
 
 // Merge: one 128-thread workgroup per (query head h = kvh*G + g, half of D),
 // grid (Hkv, 2G), linear id (2g + half) * Hkv + kvh (the split pass's XCD
-// map).  The split
-// weights 2^(m_s - M) use the hardware exp2 (v_exp_f32): it differs from the
-// library exp2f only below 2^-126, i.e. for splits whose max trails the
-// overall max by more than 126 (log2 units), whose weight is nil either way;
+// map).  The split weights 2^(m_s - M) use the hardware exp2 (v_exp_f32): it
+// differs from the library exp2f only below 2^-126, i.e. for splits whose max
+// trails the overall max by more than 126 (log2 units), whose weight is nil either way;
 // without the library's denormal path the Qwen3-32B step is ~0.2 us shorter
 // (23.91 -> 23.68 us at 32k, bit-identical output).
 // Thread t owns 4 consecutive d (one float4) and every 8th split, keeps its
