@@ -107,24 +107,9 @@ __device__ __forceinline__ void wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)
 // 15:14 = 0, expcnt bits 6:4 = 7, lgkmcnt bits 11:8 = 15, i.e. no wait).
 constexpr int kVmcnt0 = 0x0F70;
 
-// x / d for every x < 2^31 without a runtime division: (x * m) >> sh with
-// l = ceil(log2 d), m = ceil(2^(31+l) / d) < 2^32, sh = 31 + l (Granlund and
-// Montgomery, "Division by invariant integers using multiplication", 1994,
-// Thm 4.2: m d - 2^(31+l) < d <= 2^l).  The per-team kernel splits its
-// workgroup id with it, so its first loads wait for no integer division
-// (Qwen3-4B S=2048 40.62 -> 40.16 us, S=512 9.83 -> 9.73 us, bit-identical).
-struct DivBy {
-  uint32_t m;
-  int sh;
-};
-__host__ __device__ inline uint32_t div_by(uint32_t x, DivBy d) {
-  return (uint32_t)(((uint64_t)x * d.m) >> d.sh);
-}
-static DivBy make_div(int d) {
-  int l = 0;
-  while ((1ll << l) < d) ++l;
-  return DivBy{(uint32_t)(((1ull << (31 + l)) + (uint64_t)d - 1) / (uint64_t)d), 31 + l};
-}
+// The per-team kernel splits its workgroup id with host-computed multipliers
+// (DivBy), so its first loads wait for no integer division (Qwen3-4B S=2048
+// 40.62 -> 40.16 us, S=512 9.83 -> 9.73 us, bit-identical).
 // Workgroup id = (r * nsub + hsub) * Hkv + kvh, with G = Hq / Hkv query heads
 // per kv head in nsub = G / HG sub-groups.
 struct BlockMap {

@@ -52,6 +52,25 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // 2^(s - m).
 constexpr float kPHeadroom = 7.0f;
 
+// x / d for every x < 2^31 without a runtime division (one is ~20 dependent
+// instructions with a reciprocal round trip, in front of every load whose
+// address needs it): (x * m) >> sh with l = ceil(log2 d), m = ceil(2^(31+l) /
+// d) < 2^32, sh = 31 + l (Granlund and Montgomery, "Division by invariant
+// integers using multiplication", 1994, Thm 4.2: m d - 2^(31+l) < d <= 2^l).
+// The host computes (m, sh) once per launch with make_div.
+struct DivBy {
+  uint32_t m;
+  int sh;
+};
+__host__ __device__ inline uint32_t div_by(uint32_t x, DivBy d) {
+  return (uint32_t)(((uint64_t)x * d.m) >> d.sh);
+}
+inline DivBy make_div(int d) {
+  int l = 0;
+  while ((1ll << l) < d) ++l;
+  return DivBy{(uint32_t)(((1ull << (31 + l)) + (uint64_t)d - 1) / (uint64_t)d), 31 + l};
+}
+
 // Cross-lane xor shuffle within the wave (ds_bpermute based).
 __device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
