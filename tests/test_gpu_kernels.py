@@ -116,6 +116,8 @@ def _decode_case(gpu, Hq, Hkv, ctx, max_ctx, num_splits, tag):
     (40, 8, 777, 1000, None),     # G = 5
     (16, 1, 1500, 2048, None),    # one kv head (G = 16)
     (28, 4, 900, 1024, 5),        # Hkv = 4, G = 7
+    (32, 32, 600, 640, None),     # 32 kv heads (G = 1): a wide first grid dimension
+    (26, 2, 1000, 1024, 9),       # G = 13
     (32, 16, 2000, 2048, None),   # Hkv = 16, G = 2
     (12, 3, 2000, 2048, None),    # odd kv head counts: Hkv = 3, 5, 6
     (80, 5, 777, 1024, 9),        # Hkv = 5, G = 16
@@ -313,7 +315,9 @@ def test_decode_reuses_workspace_across_calls(gpu):
     (1, 32, 8, 0), (17, 32, 8, 0), (64, 16, 8, 3), (200, 32, 8, 77), (130, 64, 8, 0),
     (96, 8, 8, 10), (77, 40, 8, 9), (33, 16, 1, 0), (150, 48, 8, 5), (111, 56, 8, 0),
     (1, 32, 8, 4095), (3, 64, 8, 1000),  # a one-token extend, a short chunk after a long prefix
-    (100, 24, 3, 5), (70, 80, 5, 0), (300, 36, 6, 17)])  # Hkv = 3, 5, 6 (G = 8, 16, 6)
+    (100, 24, 3, 5), (70, 80, 5, 0), (300, 36, 6, 17),  # Hkv = 3, 5, 6 (G = 8, 16, 6)
+    (60, 40, 40, 3), (50, 26, 2, 0), (90, 39, 3, 11)])  # Hkv = 40 (G = 1); G = 13 (13 one-head
+                                                       # sub-groups per kv head, both Hkv = 2, 3)
 def test_prefill_attention_vs_oracle(gpu, S, Hq, Hkv, pos0):
     _say("prefill", S, Hq, Hkv, pos0)
     max_ctx = pos0 + S + 5
