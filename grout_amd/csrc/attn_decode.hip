@@ -314,8 +314,7 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES <= 4 ? 2 : 1)) void attn_decode_
       sc[i] = i < lim ? sc[i] * scale_log2 : -__builtin_inff();
       tmax = fmaxf(tmax, sc[i]);
     }
-    tmax = fmaxf(tmax, shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, shfl_xor(tmax, 32));
+    tmax = col_max(tmax);  // over the 4 lane groups of the column
     if (__any(tmax > m + (kDecRescaleThreshold + kPHeadroom))) {
       const float mn = fmaxf(m, tmax - kPHeadroom);
       const float alpha = fast_exp2(m - mn);
@@ -389,8 +388,7 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES <= 4 ? 2 : 1)) void attn_decode_
   // accumulators as single floats with the 16 head lanes on one LDS bank and
   // recomputed the weights per element: 1.2 + 0.75 us per wave against
   // 0.45 + 0.4 us here (Qwen3-32B, 32k context: split 22.6 -> 21.5 us).
-  l += shfl_xor(l, 16);
-  l += shfl_xor(l, 32);
+  l = col_sum(l);
   if (kb == 0) {
     s_ml[w][col][0] = m;
     s_ml[w][col][1] = l;

@@ -117,21 +117,6 @@ struct BlockMap {
   DivBy hkv, nsub;
 };
 
-// Lane l ends with f(x[l], x[l ^ 16]) and then f(.., x[l ^ 32]): the reduction
-// over the four 16-lane groups that hold one MFMA column.
-__device__ __forceinline__ float col_max(float x) {
-  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-__device__ __forceinline__ float col_sum(float x) {
-  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-
 // MB: 16-row MFMA blocks per wave (2: 32 rows per wave, 128 per team; 1: 16
 // and 64, for short prompts, where the 128-row form leaves CUs idle).
 template <int HG, int MB>

@@ -71,6 +71,22 @@ inline DivBy make_div(int d) {
   return DivBy{(uint32_t)(((1ull << (31 + l)) + (uint64_t)d - 1) / (uint64_t)d), 31 + l};
 }
 
+// Lane l ends with f(x[l], x[l ^ 16]) and then f(.., x[l ^ 32]): the reduction
+// over the four 16-lane groups that hold one MFMA column, on the VALU
+// (v_permlane16/32_swap, gfx950) instead of two LDS round trips.
+__device__ __forceinline__ float col_max(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float col_sum(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // Cross-lane xor shuffle within the wave (ds_bpermute based).
 __device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
