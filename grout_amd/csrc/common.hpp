@@ -87,7 +87,48 @@ __device__ __forceinline__ float col_sum(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// Cross-lane xor shuffle within the wave (ds_bpermute based).
-__device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
+// x of lane (lane ^ OFF), i.e. __shfl_xor(x, OFF) over the 64-lane wave, on
+// the VALU instead of an LDS round trip (ds_bpermute): across 16-lane rows
+// with v_permlane32/16_swap (each lane keeps the one of the two results
+// that came from its partner), within a row with DPP: row_ror:8 is xor 8,
+// the row half-mirror (i -> 7 - i in each 8 lanes) followed by the quad
+// reversal (i -> 3 - i in each 4) is xor 4, quad_perm [2,3,0,1] and
+// [1,0,3,2] are xor 2 and xor 1.  Every lane reads the same partner as with
+// the shuffle, so reductions built on it give the same bits.  All 64 lanes
+// must be active.
+template <int OFF>
+__device__ __forceinline__ uint32_t xor_lane_u32(uint32_t x) {
+  static_assert(OFF == 1 || OFF == 2 || OFF == 4 || OFF == 8 || OFF == 16 || OFF == 32,
+                "xor offsets 1..32");
+  if constexpr (OFF == 32 || OFF == 16) {
+    const auto a = OFF == 32 ? __builtin_amdgcn_permlane32_swap(x, x, false, false)
+                             : __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return (__lane_id() & OFF) ? a[0] : a[1];
+  } else if constexpr (OFF == 8) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x128, 0xF, 0xF, false);
+  } else if constexpr (OFF == 4) {
+    const int hm = __builtin_amdgcn_update_dpp(0, (int)x, 0x141, 0xF, 0xF, false);
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, hm, 0x1B, 0xF, 0xF, false);
+  } else {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, OFF == 2 ? 0x4E : 0xB1, 0xF, 0xF,
+                                                 false);
+  }
+}
+template <int OFF>
+__device__ __forceinline__ float xor_lane(float x) {
+  return __uint_as_float(xor_lane_u32<OFF>(__float_as_uint(x)));
+}
+// Sum over the wave in the butterfly order of x += __shfl_xor(x, off), off =
+// 32, 16, ..., 1 (the same bits).
+__device__ __forceinline__ float wave_xor_sum(float x) {
+  x += xor_lane<32>(x);
+  x += xor_lane<16>(x);
+  x += xor_lane<8>(x);
+  x += xor_lane<4>(x);
+  x += xor_lane<2>(x);
+  x += xor_lane<1>(x);
+  return x;
+}
+
 
 }  // namespace grout

@@ -20,11 +20,10 @@ namespace grout {
 
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
-  return x;
-}
+// Butterfly sum over the wave (x += x of lane ^ off, off = 32 .. 1) on the
+// VALU: it ends every GEMV, so two LDS round trips per step were on each
+// launch's critical path.
+__device__ __forceinline__ float wave_sum(float x) { return wave_xor_sum(x); }
 
 // acc + <w, x> over 8 halves with v_dot2_f32_f16 (fp32 accumulation).
 __device__ __forceinline__ float dot8(u32x4 w, half8 x, float acc) {
@@ -577,13 +576,20 @@ __device__ __forceinline__ void argmax_combine(float& m, uint32_t& i, float m2, 
     i = i2;
   }
 }
+template <int OFF>
+__device__ __forceinline__ void argmax_step(float& m, uint32_t& i) {
+  const float m2 = xor_lane<OFF>(m);
+  const uint32_t i2 = xor_lane_u32<OFF>(i);
+  argmax_combine(m, i, m2, i2);
+}
+// The butterfly over the wave (partner = lane ^ off, off = 32 .. 1).
 __device__ __forceinline__ void argmax_wave(float& m, uint32_t& i) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float m2 = __shfl_xor(m, off, 64);
-    const uint32_t i2 = (uint32_t)__shfl_xor((int)i, off, 64);
-    argmax_combine(m, i, m2, i2);
-  }
+  argmax_step<32>(m, i);
+  argmax_step<16>(m, i);
+  argmax_step<8>(m, i);
+  argmax_step<4>(m, i);
+  argmax_step<2>(m, i);
+  argmax_step<1>(m, i);
 }
 
 __global__ __launch_bounds__(256) void argmax_blocks_kernel(const half_t* __restrict__ logits,

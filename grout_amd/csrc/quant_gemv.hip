@@ -340,9 +340,9 @@ __device__ __forceinline__ void stage_x(u32x4 v, int c, int NG, half_t* s_x, flo
   float s = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; e += 2) s = __builtin_amdgcn_fdot2(half2v{h[e], h[e + 1]}, one, s, false);
-  s += __shfl_xor(s, 1, 64);
+  s += xor_lane<1>(s);
   if (FMT == 8) {
-    s += __shfl_xor(s, 2, 64);
+    s += xor_lane<2>(s);
     if (c < NG && (c & 3) == 0) s_xsum[c >> 2] = s * 0x1p-17f;
   } else if (FMT == 12 || FMT == 13) {
     if (c < NG && (c & 1) == 0) s_xsum[xsum_slot(c >> 1)] = s;
@@ -486,11 +486,7 @@ struct QNorm {
 // The residual of a norm without one (read-only zeros, never written).
 __device__ half_t kQZero[kQMaxK];
 
-__device__ __forceinline__ float qwave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
+__device__ __forceinline__ float qwave_sum(float v) { return wave_xor_sum(v); }
 
 // c of chunk (8 values) and its contribution to sum(c^2).
 __device__ __forceinline__ float qnorm_c(u32x4 xv, u32x4 rv, float (&c)[8]) {
@@ -648,8 +644,11 @@ __global__ __launch_bounds__(R * S * kQTeam) void gemv_q_kernel(const uint8_t* _
     }
   }
 
-#pragma unroll
-  for (int off = 8; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 16);
+  // the team's 16 lanes, butterfly order (lane ^ 8, 4, 2, 1), on the VALU
+  acc += xor_lane<8>(acc);
+  acc += xor_lane<4>(acc);
+  acc += xor_lane<2>(acc);
+  acc += xor_lane<1>(acc);
   if constexpr (S > 1) {
     // slice partials summed in slice order by slice 0
     float* const s_red = s_sc + R * SCW;
@@ -661,7 +660,7 @@ __global__ __launch_bounds__(R * S * kQTeam) void gemv_q_kernel(const uint8_t* _
     for (int w = 1; w < S; ++w) acc += s_red[w * R + team];
   }
   if (SILU) {
-    const float up = __shfl_xor(acc, 32, 64);  // gate teams 0, 1 <-> up teams 2, 3
+    const float up = xor_lane<32>(acc);  // gate teams 0, 1 <-> up teams 2, 3
     if (m == 0 && (team & 3) < 2 && out < N) {
       const half_t g = (half_t)acc, u = (half_t)up;
       const float gf = (float)g;
