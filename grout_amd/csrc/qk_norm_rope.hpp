@@ -111,8 +111,9 @@ __device__ __forceinline__ u32x2 norm_rope_row(u32x2 xr, half4 gh, floatx4 c, fl
 // two lane values.  IEEE addition commutes, so every sum equals the 32-lane
 // tree's bit for bit.  All 8 lanes of the group must be active.
 __device__ __forceinline__ float xor_lane4(float x) {
-  // ds_swizzle bitmask mode: and 0x1f, or 0, xor 4
-  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x101f));
+  // DPP row half-mirror then quad reversal (common.hpp), the same partner as
+  // the ds_swizzle xor-4 mode without its LDS round trip
+  return xor_lane<4>(x);
 }
 __device__ __forceinline__ float xor_lane2(float x) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4e, 0xf, 0xf, false));
